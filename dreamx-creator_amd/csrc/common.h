@@ -1,0 +1,63 @@
+// Shared helpers for the libsrdit_hip kernels: status reporting, vector types,
+// alignment checks.  gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "srdit_hip.h"
+
+namespace srdit {
+
+// Per-thread message of the last failure, read back by srdit_last_error().
+void set_error(const char* fmt, ...);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+#define SRDIT_REQUIRE(cond, ...)           \
+  do {                                     \
+    if (!(cond)) {                         \
+      ::srdit::set_error(__VA_ARGS__);     \
+      return SRDIT_EINVAL;                 \
+    }                                      \
+  } while (0)
+
+#define SRDIT_HIP_CHECK(expr)                                                        \
+  do {                                                                               \
+    hipError_t e_ = (expr);                                                          \
+    if (e_ != hipSuccess) {                                                          \
+      ::srdit::set_error("%s failed: %s", #expr, hipGetErrorString(e_));             \
+      return SRDIT_EHIP;                                                             \
+    }                                                                                \
+  } while (0)
+
+// Launch-error check after <<<>>>: reports configuration errors synchronously.
+#define SRDIT_LAUNCH_CHECK(what)                                                     \
+  do {                                                                               \
+    hipError_t e_ = hipGetLastError();                                               \
+    if (e_ != hipSuccess) {                                                          \
+      ::srdit::set_error("%s launch failed: %s", what, hipGetErrorString(e_));       \
+      return SRDIT_EHIP;                                                             \
+    }                                                                                \
+  } while (0)
+
+typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
+typedef short s16x4_t __attribute__((__vector_size__(4 * sizeof(short))));
+typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
+typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
+typedef int i32x8_t __attribute__((__vector_size__(8 * sizeof(int))));
+typedef int i32x4_t __attribute__((__vector_size__(4 * sizeof(int))));
+typedef int i32x2_t __attribute__((__vector_size__(2 * sizeof(int))));
+
+// XCD-contiguous task index.  Workgroups are dispatched round-robin over the
+// 8 XCDs (workgroup b runs on XCD b % 8); this bijection on [0, n) gives each
+// XCD one contiguous range of tasks so neighbouring tasks share that XCD's L2.
+__device__ __forceinline__ uint32_t xcd_task(uint32_t bid, uint32_t n) {
+  const uint32_t x = bid & 7u, slot = bid >> 3;
+  return x * (n >> 3) + (x < (n & 7u) ? x : (n & 7u)) + slot;
+}
+
+}  // namespace srdit

@@ -1,0 +1,456 @@
+// Block-grid window attention forward for gfx950 (MI355X).
+//
+// One wavefront owns one task = (window, 64-query tile, head).  It walks the
+// window's KV cuboid 32 keys per step with an online softmax:
+//
+//   S^T[32 keys x 32 queries] = K[32 x D] . Q^T[D x 32]      (v_mfma 32x32x16)
+//   O^T[D x 32 queries]      += V^T[D x 32 keys] . P^T[32 x 32]
+//
+// Computing S transposed puts one query per lane (column = lane % 32), so the
+// softmax statistics are lane-local: a lane and its partner lane+32 hold the
+// same query's 16+16 keys, and one permlane32 swap combines them.  The S^T
+// accumulator registers feed the P^T operand of the second MFMA directly (the
+// contraction over keys uses the accumulator's own key order), and V^T comes
+// out of LDS with ds_read_b64_tr_b16, so no shuffles are needed anywhere.
+//
+// Semantics follow the reference kernels
+// (video_refiner/wan/modules/sr_dit/blockgrid_triton.py:184-278 plain,
+//  :281-389 per-frame anchor): scale applied to q.k in fp32, masked keys never
+// contribute, a fully masked tile leaves the running statistics unchanged,
+// P is rounded to the input dtype before P.V, fp32 accumulation, O = acc / l.
+// The exponential is evaluated as exp2 of log2(e)-scaled logits.
+
+#include "common.h"
+
+namespace srdit {
+namespace {
+
+template <typename T> struct Elem;
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Eight fp32 values -> one 8-element MFMA operand, converted two at a time
+// (v_cvt_pk_*) and assembled as whole 32-bit registers.
+template <typename H2, typename V8>
+__device__ __forceinline__ V8 pack8_impl(const float* x) {
+  i32x4_t w;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const f32x2_t f = {x[2 * j], x[2 * j + 1]};
+    w[j] = __builtin_bit_cast(int, __builtin_convertvector(f, H2));
+  }
+  return __builtin_bit_cast(V8, w);
+}
+
+template <> struct Elem<__bf16> {
+  typedef bf16x8_t v8;
+  typedef bf16x2_t h2;
+  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<bf16x2_t, v8>(x); }
+};
+template <> struct Elem<_Float16> {
+  typedef f16x8_t v8;
+  typedef f16x2_t h2;
+  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<f16x2_t, v8>(x); }
+};
+
+struct WinArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  const int32_t* params;
+  const int32_t* order;
+  int n_w, m_tiles, p_stride, hr_base, H, W;
+  int64_t q_tokens, kv_tokens;
+  int n_heads;
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+constexpr int QT = 2;   // 32-query MFMA tiles per wavefront
+constexpr int KN = 32;  // keys per step
+
+// n / d for 0 <= n < 2^22, d > 0, rd = 1/d: float estimate plus one correction.
+__device__ __forceinline__ int fdiv(int n, int d, float rd) {
+  int qv = static_cast<int>(static_cast<float>(n) * rd);
+  const int r = n - qv * d;
+  qv += (r >= d) - (r < 0);
+  return qv;
+}
+
+__device__ __forceinline__ float other_half_max(float x) {
+  i32x2_t s = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(__int_as_float(s[0]), __int_as_float(s[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  i32x2_t s = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return __int_as_float(s[0]) + __int_as_float(s[1]);
+}
+
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// One contiguous run of keys with a common decode.
+//   kind 0: HR cuboid   flat = base + (t0 + j/sp)*L + (r0 + (j%sp)/cw)*Wg + c0 + (j%sp)%cw
+//   the anchor prefix of the plain kernel and an anchor segment of the frame
+//   kernel are the same formula with their own grid and a frame base.
+struct KeyRun {
+  int n;          // keys in the run
+  int64_t base;   // token offset of frame 0 of the run
+  int frame_len;  // tokens per frame of the grid the run lives on
+  int t0, r0, c0; // first frame / row / column
+  int rows, cols; // cuboid rows / columns per frame
+  int Wg;         // grid width (row stride in tokens)
+  float r_sp, r_cols;
+};
+
+__device__ __forceinline__ KeyRun make_run(int n, int64_t base, int frame_len, int t0, int r0,
+                                           int c0, int rows, int cols, int Wg) {
+  KeyRun k;
+  k.n = n; k.base = base; k.frame_len = frame_len; k.t0 = t0; k.r0 = r0; k.c0 = c0;
+  k.rows = rows; k.cols = cols; k.Wg = Wg;
+  k.r_sp = 1.0f / static_cast<float>(rows * cols);
+  k.r_cols = 1.0f / static_cast<float>(cols);
+  return k;
+}
+
+__device__ __forceinline__ int64_t run_token(const KeyRun& k, int j) {
+  const int sp = k.rows * k.cols;
+  const int t = fdiv(j, sp, k.r_sp);
+  const int rr = j - t * sp;
+  const int row = fdiv(rr, k.cols, k.r_cols);
+  const int col = rr - row * k.cols;
+  return k.base + static_cast<int64_t>(k.t0 + t) * k.frame_len +
+         static_cast<int64_t>(k.r0 + row) * k.Wg + (k.c0 + col);
+}
+
+template <typename T, int D>
+struct Tile {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  static constexpr int KS = D / 16;  // k-steps of the S^T MFMA over the head dim
+  static constexpr int DT = D / 32;  // 32-row tiles of O^T over the head dim
+  static constexpr int VS = D + 8;   // LDS row stride of the staged V tile (elements)
+  static constexpr int HD = D / 2;   // head-dim elements per lane half
+
+  V8 qf[QT][KS];
+  f32x16_t oacc[QT][DT];
+  float mrun[QT], lrun[QT];
+};
+
+// Walk one key run: online softmax over 32-key steps.  `seg` >= 0 restricts
+// the run to queries of frame `seg` (per-frame anchor), -1 admits all.
+template <typename T, int D>
+__device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, int seg,
+                                           const int (&qframe)[QT], const bool (&qvalid)[QT],
+                                           const T* __restrict__ kb, const T* __restrict__ vb,
+                                           int64_t tok, int64_t kv_tokens, float scale_log2,
+                                           T* vsh) {
+  using TT = Tile<T, D>;
+  using E = typename TT::E;
+  using V8 = typename TT::V8;
+  constexpr int KS = TT::KS, DT = TT::DT, VS = TT::VS, HD = TT::HD;
+  if (run.n <= 0) return;
+  const int lane = threadIdx.x;
+  const int c = lane & 31, hf = lane >> 5;
+
+  bool admit[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) admit[qt] = (seg < 0) || (qvalid[qt] && qframe[qt] == seg);
+  if (seg >= 0) {
+    // Skip the run if no query of this tile belongs to the segment.
+    bool any = false;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) any |= admit[qt];
+    if (!__any(any)) return;
+  }
+
+  auto load_kv = [&](int s0, V8 (&kf)[KS], V8 (&vf)[KS]) {
+    const int j = s0 + c;
+    const bool ok = j < run.n;
+    int64_t flat = run_token(run, ok ? j : run.n - 1);
+    flat = flat < 0 ? 0 : (flat >= kv_tokens ? kv_tokens - 1 : flat);
+    const V8* kp = reinterpret_cast<const V8*>(kb + flat * tok + hf * HD);
+    const V8* vp = reinterpret_cast<const V8*>(vb + flat * tok + hf * HD);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = kp[ks];
+      vf[ks] = vp[ks];
+    }
+    if (!ok) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) vf[ks] = V8{};
+    }
+  };
+
+  V8 kcur[KS], vcur[KS];
+  load_kv(0, kcur, vcur);
+  for (int s0 = 0; s0 < run.n; s0 += KN) {
+    V8 knext[KS], vnext[KS];
+    const bool more = s0 + KN < run.n;
+    if (more) load_kv(s0 + KN, knext, vnext);
+
+    // stage V: lane (c, hf) holds key c, head dims [hf*HD, hf*HD + HD)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      *reinterpret_cast<V8*>(vsh + c * VS + hf * HD + ks * 8) = vcur[ks];
+
+    // S^T = K . Q^T
+    f32x16_t sacc[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) sacc[qt] = f32x16_t{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) sacc[qt] = E::mma(kcur[ks], st.qf[qt][ks], sacc[qt]);
+
+    // online softmax, one query per lane
+    V8 pf[QT][2];
+    const int nvalid = run.n - s0;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float sv[16];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = 8 * (r >> 2) + 4 * hf + (r & 3);
+        sv[r] = (key < nvalid && admit[qt]) ? sacc[qt][r] * scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sv[r]);
+      }
+      mx = other_half_max(mx);
+      const float mnew = fmaxf(st.mrun[qt], mx);
+      const bool live = mnew != -INFINITY;
+      const float alpha = live ? __builtin_amdgcn_exp2f(st.mrun[qt] - mnew) : 1.0f;
+      float psum = 0.f;
+      float pv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pv[r] = live ? __builtin_amdgcn_exp2f(sv[r] - mnew) : 0.f;
+        psum += pv[r];
+      }
+      st.lrun[qt] = st.lrun[qt] * alpha + psum;
+      st.mrun[qt] = mnew;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) st.oacc[qt][dt] *= alpha;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) pf[qt][kk] = E::pack8(&pv[kk * 8]);
+    }
+
+    __syncthreads();  // staged V visible to every lane
+
+    // O^T += V^T . P^T ; V^T operand via transposing LDS reads
+    const int g = lane >> 4, i16 = lane & 15;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int dimbase = dt * 32 + 16 * (g & 1);
+        i32x2_t half[2];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int keybase = 16 * kk + 8 * h2 + 4 * hf;
+          const T* src = vsh + (keybase + (i16 >> 2)) * VS + dimbase + 4 * (i16 & 3);
+          half[h2] = __builtin_bit_cast(
+              i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(const_cast<T*>(src))));
+        }
+        const i32x4_t vw = {half[0][0], half[0][1], half[1][0], half[1][1]};
+        const V8 vt = __builtin_bit_cast(V8, vw);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) st.oacc[qt][dt] = E::mma(vt, pf[qt][kk], st.oacc[qt][dt]);
+      }
+    }
+    __syncthreads();  // reads done before the next step restages V
+
+    if (more) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        kcur[ks] = knext[ks];
+        vcur[ks] = vnext[ks];
+      }
+    }
+  }
+}
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(64) void window_attn_kernel(WinArgs a) {
+  using TT = Tile<T, D>;
+  using E = typename TT::E;
+  using V8 = typename TT::V8;
+  constexpr int KS = TT::KS, DT = TT::DT, VS = TT::VS, HD = TT::HD;
+  __shared__ __attribute__((aligned(16))) T vsh[KN * VS];
+
+  const int lane = threadIdx.x;
+  const int c = lane & 31, hf = lane >> 5;
+  const uint32_t task = xcd_task(blockIdx.x, gridDim.x);
+  const int head = static_cast<int>(task % static_cast<uint32_t>(a.n_heads));
+  const uint32_t rest = task / static_cast<uint32_t>(a.n_heads);
+  const int mt = static_cast<int>(rest % static_cast<uint32_t>(a.m_tiles));
+  const uint32_t wslot = rest / static_cast<uint32_t>(a.m_tiles);
+  if (wslot >= static_cast<uint32_t>(a.n_w)) return;
+  int wid = a.order[wslot];
+  wid = wid < 0 ? 0 : (wid >= a.n_w ? a.n_w - 1 : wid);
+  const int32_t* p = a.params + static_cast<int64_t>(wid) * a.p_stride;
+
+  int q_t0, q_tl, q_h0, q_w0, qh_l, qw_l, kv_t0, kv_tl, kh0, kh_l, kw0, kw_l, a_frames;
+  int kh0_a, kh_l_a, kw0_a, kw_l_a, h_a, w_a;
+  if (MODE == 0) {
+    q_t0 = p[0]; q_tl = p[1]; q_h0 = p[2]; q_w0 = p[3]; qh_l = p[4]; qw_l = p[5];
+    kv_t0 = p[6]; kv_tl = p[7]; kh0 = p[8]; kh_l = p[9]; kw0 = p[10]; kw_l = p[11];
+    a_frames = p[12]; kh0_a = p[13]; kh_l_a = p[14]; kw0_a = p[15]; kw_l_a = p[16];
+    h_a = p[17]; w_a = p[18];
+  } else {
+    q_t0 = 0; q_h0 = p[0]; q_w0 = p[1]; qh_l = p[2]; qw_l = p[3];
+    kv_t0 = p[4]; kv_tl = p[5]; kh0 = p[6]; kh_l = p[7]; kw0 = p[8]; kw_l = p[9];
+    q_tl = p[10]; a_frames = 0; kh0_a = p[11]; kh_l_a = p[12]; kw0_a = p[13]; kw_l_a = p[14];
+    h_a = p[15]; w_a = p[16];
+  }
+  const int q_sp = qh_l * qw_l;
+  const int lq = q_tl * q_sp;
+  const int m0 = mt * 64;
+  if (q_sp <= 0 || q_tl <= 0 || m0 >= lq) return;
+
+  const int L = a.H * a.W;
+  const int64_t tok = static_cast<int64_t>(a.n_heads) * D;
+  const T* qb = reinterpret_cast<const T*>(a.q) + head * D;
+  const T* kb = reinterpret_cast<const T*>(a.k) + head * D;
+  const T* vb = reinterpret_cast<const T*>(a.v) + head * D;
+  T* ob = reinterpret_cast<T*>(a.o) + head * D;
+
+  TT st;
+  int64_t qflat[QT];
+  int qframe[QT];
+  bool qvalid[QT];
+  const float r_qsp = 1.0f / static_cast<float>(q_sp), r_qw = 1.0f / static_cast<float>(qw_l);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int m = m0 + qt * 32 + c;
+    qvalid[qt] = m < lq;
+    const int mm = qvalid[qt] ? m : 0;
+    const int t = fdiv(mm, q_sp, r_qsp);
+    const int r = mm - t * q_sp;
+    const int hh = fdiv(r, qw_l, r_qw);
+    const int ww = r - hh * qw_l;
+    int64_t flat = static_cast<int64_t>(q_t0 + t) * L + static_cast<int64_t>(q_h0 + hh) * a.W + (q_w0 + ww);
+    flat = flat < 0 ? 0 : (flat >= a.q_tokens ? a.q_tokens - 1 : flat);
+    qflat[qt] = flat;
+    qframe[qt] = t;
+    const V8* qp = reinterpret_cast<const V8*>(qb + flat * tok + hf * HD);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) st.qf[qt][ks] = qvalid[qt] ? qp[ks] : V8{};
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) st.oacc[qt][dt] = f32x16_t{};
+    st.mrun[qt] = -INFINITY;
+    st.lrun[qt] = 0.f;
+  }
+
+  const int sp_hr = kh_l * kw_l;
+  const int sp_a = kh_l_a * kw_l_a;
+  const bool anchor_ok = kh_l_a > 0 && kw_l_a > 0 && h_a > 0 && w_a > 0;
+  if (MODE == 0) {
+    // anchor prefix (a_frames whole-chunk anchor frames), then the HR cuboid
+    if (a_frames > 0 && anchor_ok) {
+      KeyRun ar = make_run(a_frames * sp_a, 0, h_a * w_a, 0, kh0_a, kw0_a, kh_l_a, kw_l_a, w_a);
+      attend_run<T, D>(st, ar, -1, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2, vsh);
+    }
+    if (sp_hr > 0 && kv_tl > 0) {
+      KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
+      attend_run<T, D>(st, hr, -1, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2, vsh);
+    }
+  } else {
+    // per-frame anchor: query frame s sees anchor frame s only, over the
+    // frames this tile holds; then the shared HR cuboid
+    if (anchor_ok) {
+      const int f_lo = m0 / q_sp;
+      const int f_hi = (min(lq, m0 + 64) - 1) / q_sp;
+      for (int s = f_lo; s <= f_hi; ++s) {
+        KeyRun ar = make_run(sp_a, static_cast<int64_t>(s) * h_a * w_a, h_a * w_a, 0, kh0_a, kw0_a,
+                             kh_l_a, kw_l_a, w_a);
+        attend_run<T, D>(st, ar, s, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2, vsh);
+      }
+    }
+    if (sp_hr > 0 && kv_tl > 0) {
+      KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
+      attend_run<T, D>(st, hr, -1, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2, vsh);
+    }
+  }
+
+  // O = acc / l ; lane (c, hf) writes dims dt*32 + 8*g4 + 4*hf + [0, 4)
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const float lt = half_sum(st.lrun[qt]);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    if (!qvalid[qt]) continue;
+    T* op = ob + qflat[qt] * tok;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const f32x2_t lo = {st.oacc[qt][dt][g4 * 4 + 0] * inv, st.oacc[qt][dt][g4 * 4 + 1] * inv};
+        const f32x2_t hi = {st.oacc[qt][dt][g4 * 4 + 2] * inv, st.oacc[qt][dt][g4 * 4 + 3] * inv};
+        const i32x2_t w = {__builtin_bit_cast(int, __builtin_convertvector(lo, typename E::h2)),
+                           __builtin_bit_cast(int, __builtin_convertvector(hi, typename E::h2))};
+        *reinterpret_cast<i32x2_t*>(op + dt * 32 + g4 * 8 + hf * 4) = w;
+      }
+  }
+}
+
+template <typename T, int D>
+int launch_window(const WinArgs& a, int mode, uint32_t grid, hipStream_t stream) {
+  if (mode == 0)
+    hipLaunchKernelGGL((window_attn_kernel<T, D, 0>), dim3(grid), dim3(64), 0, stream, a);
+  else
+    hipLaunchKernelGGL((window_attn_kernel<T, D, 1>), dim3(grid), dim3(64), 0, stream, a);
+  SRDIT_LAUNCH_CHECK("window_attn_kernel");
+  return SRDIT_OK;
+}
+
+}  // namespace
+}  // namespace srdit
+
+extern "C" int srdit_window_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                                     const int32_t* params, const int32_t* order, int n_w,
+                                     int m_tiles, int p_stride, int hr_base, int H, int W,
+                                     int64_t q_tokens, int64_t kv_tokens, int n_heads,
+                                     int head_dim, float scale, int mode, int dtype,
+                                     void* stream) {
+  using namespace srdit;
+  SRDIT_REQUIRE(q && k && v && o && params && order, "srdit_window_attn_fwd: null pointer");
+  SRDIT_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
+                "srdit_window_attn_fwd: q/k/v/o must be 16-byte aligned");
+  SRDIT_REQUIRE(mode == 0 || mode == 1, "srdit_window_attn_fwd: mode must be 0 or 1, got %d", mode);
+  SRDIT_REQUIRE(p_stride == (mode == 0 ? 19 : 17),
+                "srdit_window_attn_fwd: p_stride %d does not match mode %d", p_stride, mode);
+  SRDIT_REQUIRE(n_w >= 1 && m_tiles >= 1 && n_heads >= 1 && H >= 1 && W >= 1 && hr_base >= 0,
+                "srdit_window_attn_fwd: bad sizes (n_w=%d m_tiles=%d n_heads=%d H=%d W=%d hr_base=%d)",
+                n_w, m_tiles, n_heads, H, W, hr_base);
+  SRDIT_REQUIRE(q_tokens >= 1 && kv_tokens >= 1 && q_tokens < (1LL << 31) && kv_tokens < (1LL << 31),
+                "srdit_window_attn_fwd: token counts out of range");
+  SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 30), "srdit_window_attn_fwd: grid too large");
+  if (head_dim != 64 && head_dim != 128) {
+    set_error("srdit_window_attn_fwd: head_dim %d unsupported (64 or 128)", head_dim);
+    return SRDIT_EUNSUPPORTED;
+  }
+  if (dtype != SRDIT_DTYPE_BF16 && dtype != SRDIT_DTYPE_FP16) {
+    set_error("srdit_window_attn_fwd: dtype code %d unsupported", dtype);
+    return SRDIT_EUNSUPPORTED;
+  }
+  const int64_t grid64 = static_cast<int64_t>(n_w) * m_tiles * n_heads;
+  SRDIT_REQUIRE(grid64 < (1LL << 31), "srdit_window_attn_fwd: too many tasks");
+  WinArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o; a.params = params; a.order = order;
+  a.n_w = n_w; a.m_tiles = m_tiles; a.p_stride = p_stride; a.hr_base = hr_base; a.H = H; a.W = W;
+  a.q_tokens = q_tokens; a.kv_tokens = kv_tokens; a.n_heads = n_heads;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const uint32_t grid = static_cast<uint32_t>(grid64);
+  if (dtype == SRDIT_DTYPE_BF16)
+    return head_dim == 128 ? launch_window<__bf16, 128>(a, mode, grid, s)
+                           : launch_window<__bf16, 64>(a, mode, grid, s);
+  return head_dim == 128 ? launch_window<_Float16, 128>(a, mode, grid, s)
+                         : launch_window<_Float16, 64>(a, mode, grid, s);
+}

@@ -1,0 +1,208 @@
+"""Block-grid window attention: params-row planner and the HIP launcher.
+
+The planner turns one window geometry (a ``_BlockGridSpec``) into ONE int32
+params table, one row per query window, plus the launch tiling. The table
+layout, the row order and the ``block_m``/``m_tiles``/``hr_base``/``p_stride``
+values are the reference's launch contract
+(video_refiner/wan/modules/sr_dit/blockgrid_triton.py:68-150), kept bit-exact so
+a plan built here and a plan built by the reference are interchangeable.
+
+The launcher (:func:`run_blockgrid_hip`, the counterpart of
+``run_blockgrid_triton``, blockgrid_triton.py:392-422) hands the table to the
+HIP kernel through the C ABI in ``libsrdit_hip.so``.  There is no CPU path and
+no fallback: a missing library raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+# Params row layouts (int32, one row per window); the kernel reads them with
+# raw pointer arithmetic.  All lengths are lengths, not end indices.
+#   plain (19): q_t0 q_tL q_h0 q_w0 qhL qwL kv_t0 kv_tL kh0 khL kw0 kwL a_frames
+#               kh0_a khL_a kw0_a kwL_a H_a W_a
+#   frame (17): q_h0 q_w0 qhL qwL kv_t0 kv_tL kh0 khL kw0 kwL f_cur
+#               kh0_a khL_a kw0_a kwL_a H_a W_a
+# (field order: blockgrid_triton.py:77-80, rows: :127-141)
+P_PLAIN = 19
+P_FRAME = 17
+
+#: Query rows handled by one wavefront of the HIP kernel (two 32-row MFMA tiles).
+HIP_BLOCK_M = 64
+
+
+def _next_pow2(x: int) -> int:
+    p = 1
+    while p < x:
+        p <<= 1
+    return p
+
+
+def build_plan(spec, *, anchor_mode=None, block_n=64):
+    """One launch spec covering every window of ``spec``.
+
+    Returns ``{"params": int32 [Nw, P] (CPU), "n_w", "block_m", "m_tiles",
+    "block_n", "hr_base", "p_stride"}`` exactly as blockgrid_triton.py:83-150
+    does.  ``spec`` is read only through ``temporal_runs()``, ``h_blocks()``,
+    ``w_blocks()``, the optional ``anchor_h_blocks()``/``anchor_w_blocks()``/
+    ``anchor_grid`` and ``f_cur``/``h``/``w``.
+
+    ``anchor_mode``: ``"frame"`` (per-frame anchor, 17-field rows, the query
+    time axis must be the single run ``[0, f_cur)``), ``"chunk"`` (whole anchor
+    chunk visible, ``a_frames = f_cur``) or ``None`` (no anchor).
+    """
+    hb, wb = spec.h_blocks(), spec.w_blocks()
+    hb_a = spec.anchor_h_blocks() if hasattr(spec, "anchor_h_blocks") else hb
+    wb_a = spec.anchor_w_blocks() if hasattr(spec, "anchor_w_blocks") else wb
+    a_h, a_w = getattr(spec, "anchor_grid", (int(spec.h), int(spec.w)))
+    runs = spec.temporal_runs()
+    f_cur = int(spec.f_cur)
+
+    rows: list[list[int]] = []
+    lqs: list[int] = []
+    if anchor_mode == "frame":
+        if len(runs) != 1 or runs[0][0] != 0 or runs[0][1] != f_cur:
+            raise ValueError(
+                f'anchor_mode="frame" needs the query time axis to be the single '
+                f"run [0, {f_cur}); got {runs}.  Frame rows carry no q_t0, so a "
+                f"partitioned query axis needs anchor_mode=None or 'chunk'.")
+        kv0, kv1 = runs[0][2], runs[0][3]
+        for (qh0, qhL, kh0, khL), (_, _, kh0a, khLa) in zip(hb, hb_a):
+            for (qw0, qwL, kw0, kwL), (_, _, kw0a, kwLa) in zip(wb, wb_a):
+                rows.append([qh0, qw0, qhL, qwL, kv0, kv1 - kv0,
+                             kh0, khL, kw0, kwL, f_cur,
+                             kh0a, khLa, kw0a, kwLa, a_h, a_w])
+                lqs.append(f_cur * qhL * qwL)
+    else:
+        a_frames = f_cur if anchor_mode == "chunk" else 0
+        for (q0, q1, kv0, kv1) in runs:
+            for (qh0, qhL, kh0, khL), (_, _, kh0a, khLa) in zip(hb, hb_a):
+                for (qw0, qwL, kw0, kwL), (_, _, kw0a, kwLa) in zip(wb, wb_a):
+                    rows.append([q0, q1 - q0, qh0, qw0, qhL, qwL,
+                                 kv0, kv1 - kv0, kh0, khL, kw0, kwL, a_frames,
+                                 kh0a, khLa, kw0a, kwLa, a_h, a_w])
+                    lqs.append((q1 - q0) * qhL * qwL)
+
+    # Shared tile height: the largest window, at least 16 and at most 64 rows.
+    block_m = max(16, min(_next_pow2(max(lqs)), 64))
+    m_tiles = max(-(-x // block_m) for x in lqs)
+    return {"params": torch.tensor(rows, dtype=torch.int32).contiguous(),
+            "n_w": len(rows), "block_m": block_m, "m_tiles": m_tiles,
+            "block_n": block_n,
+            "hr_base": (f_cur * a_h * a_w) if anchor_mode is not None else 0,
+            "p_stride": P_FRAME if anchor_mode == "frame" else P_PLAIN}
+
+
+#: Plans memoised on the geometry (``tuple(spec)``), the anchor mode and
+#: ``block_n``.  Keyed on the geometry, not on the temporal rule it implies: a
+#: caller that swaps ``temporal_runs`` must clear it.
+HIP_PLAN_CACHE: dict = {}
+
+
+def cached_plan(spec, *, anchor_mode=None, block_n=64):
+    """:func:`build_plan`, memoised (blockgrid_triton.py:158-167)."""
+    key = (tuple(spec), anchor_mode, block_n)
+    plan = HIP_PLAN_CACHE.get(key)
+    if plan is None:
+        plan = HIP_PLAN_CACHE[key] = build_plan(
+            spec, anchor_mode=anchor_mode, block_n=block_n)
+    return plan
+
+
+def clear_plan_cache():
+    HIP_PLAN_CACHE.clear()
+
+
+def hip_kernel_keys(plan, *, anchor_mode=None, d=None):
+    """The kernel variants a plan launches: one, by construction.
+
+    The HIP kernels are compiled ahead of time, so this is the set of
+    (mode, query tile, head dim) instantiations the launch selects
+    (the counterpart of ``triton_compile_keys``, blockgrid_triton.py:170-181).
+    """
+    return {("frame" if anchor_mode == "frame" else "plain", HIP_BLOCK_M, d)}
+
+
+def kernel_m_tiles(plan) -> int:
+    """Query tiles of :data:`HIP_BLOCK_M` rows needed by the largest window.
+
+    Every window has at most ``block_m * m_tiles`` query rows, so this many
+    64-row tiles cover it.
+    """
+    return max(1, -(-(plan["block_m"] * plan["m_tiles"]) // HIP_BLOCK_M))
+
+
+def _window_cost(plan) -> torch.Tensor:
+    """Useful MACs per window (Lq * Lkv), the launch-order key."""
+    p = plan["params"].to(torch.int64)
+    if plan["p_stride"] == P_FRAME:
+        qsp = p[:, 2] * p[:, 3]
+        lq = p[:, 10] * qsp
+        lkv = p[:, 5] * p[:, 7] * p[:, 9] + p[:, 12] * p[:, 14]
+    else:
+        qsp = p[:, 4] * p[:, 5]
+        lq = p[:, 1] * qsp
+        lkv = p[:, 7] * p[:, 9] * p[:, 11] + p[:, 12] * p[:, 14] * p[:, 16]
+    return lq * lkv
+
+
+def launch_order(plan) -> torch.Tensor:
+    """Window launch order: most expensive first (longest-processing-time).
+
+    Edge windows are up to 4x cheaper than interior ones; launching the
+    expensive ones first keeps the last wave of workgroups short.  Ties keep
+    the planner's row order, so neighbouring windows stay adjacent in time.
+    """
+    cost = _window_cost(plan)
+    idx = torch.arange(cost.numel(), dtype=torch.int64)
+    # stable sort on -cost
+    order = sorted(range(cost.numel()), key=lambda i: (-int(cost[i]), i))
+    return torch.tensor(order, dtype=torch.int32) if order else idx.to(torch.int32)
+
+
+def _device_tables(plan, device):
+    """(params, order) on ``device``, copied once per plan and device."""
+    key = ("dev", device)
+    tabs = plan.get(key)
+    if tabs is None:
+        params = plan["params"].to(device)
+        order = launch_order(plan).to(device)
+        tabs = plan[key] = (params, order)
+    return tabs
+
+
+def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
+                      anchor_mode=None):
+    """Launch the fused window kernel for one sample; writes ``out`` and returns it.
+
+    ``q``/``out``: ``[f_cur*h*w, n, d]``.  ``k_ext``/``v_ext``: the extended KV,
+    ``cat([anchor, HR])`` when an anchor is present (``hr_base`` tokens of
+    anchor first), else the HR KV alone.  All four must be contiguous with a
+    stride-1 head dim, on one device, bf16 or fp16.  The launch is
+    asynchronous on the current stream.
+    """
+    for name, t in (("q", q), ("k_ext", k_ext), ("v_ext", v_ext), ("out", out)):
+        if not t.is_cuda:
+            raise RuntimeError(f"run_blockgrid_hip: {name} is not a GPU tensor.")
+        if not t.is_contiguous():
+            raise ValueError(f"run_blockgrid_hip: {name} must be contiguous.")
+        if t.dtype != q.dtype:
+            raise ValueError(f"run_blockgrid_hip: {name} dtype {t.dtype} != q dtype {q.dtype}.")
+        if t.dim() != 3 or t.shape[1] != n or t.shape[2] != d:
+            raise ValueError(f"run_blockgrid_hip: {name} must be [tokens, {n}, {d}], got {tuple(t.shape)}.")
+    if q.shape != out.shape or q.shape[0] != f_cur * h * w:
+        raise ValueError(f"run_blockgrid_hip: q/out must be [{f_cur * h * w}, {n}, {d}].")
+    if k_ext.shape != v_ext.shape:
+        raise ValueError("run_blockgrid_hip: k_ext and v_ext shapes differ.")
+    params, order = _device_tables(plan, q.device)
+    hr_base = plan.get("hr_base", f_cur * h * w if anchor_mode is not None else 0)
+    mode = 1 if anchor_mode == "frame" else 0
+    if (plan["p_stride"] == P_FRAME) != (mode == 1):
+        raise ValueError("run_blockgrid_hip: plan layout does not match anchor_mode.")
+    _lib.window_attn_fwd(
+        q, k_ext, v_ext, out, params, order,
+        n_w=plan["n_w"], m_tiles=kernel_m_tiles(plan), p_stride=plan["p_stride"],
+        hr_base=hr_base, H=h, W=w, n_heads=n, head_dim=d,
+        kv_tokens=k_ext.shape[0], scale=d ** -0.5, mode=mode)
+    return out

@@ -1,0 +1,112 @@
+/*
+ * srdit_hip.h -- C ABI of libsrdit_hip.so, the MI355X (gfx950) kernels behind
+ * the SR-DiT refiner's block-grid window attention and fp8 linears.
+ *
+ * Plain pointers, sizes and a hipStream_t passed as void*; no framework types.
+ * Every entry point returns 0 on success and a nonzero status on failure;
+ * srdit_last_error() returns the message of the last failure on the calling
+ * thread.  Launches are asynchronous on `stream`; nothing allocates device
+ * memory unless its comment says so.  Device pointers must be 16-byte aligned.
+ */
+#ifndef SRDIT_HIP_H
+#define SRDIT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define SRDIT_OK 0
+#define SRDIT_EINVAL 1       /* bad argument (shape, alignment, mode, null pointer) */
+#define SRDIT_EHIP 2         /* a HIP runtime call failed */
+#define SRDIT_EUNSUPPORTED 3 /* valid but not implemented (dtype, head dim) */
+
+/* element type codes */
+#define SRDIT_DTYPE_BF16 0
+#define SRDIT_DTYPE_FP16 1
+
+/*
+ * Block-grid window attention, forward.
+ *
+ * Replaces the launch of the fused window kernels in
+ * video_refiner/wan/modules/sr_dit/blockgrid_triton.py:392-422
+ * (run_blockgrid_triton -> _blockgrid_fused_kernel :184-278 for mode 0,
+ *  _blockgrid_fused_frame_kernel :281-389 for mode 1).
+ *
+ * q, o        [q_tokens, n_heads, head_dim]  (token stride n_heads*head_dim)
+ * k, v        [kv_tokens, n_heads, head_dim] (anchor prefix of hr_base tokens,
+ *                                             then the HR KV)
+ * params      int32 [n_w, p_stride] device table, the planner's rows
+ *             (p_stride 19 for mode 0, 17 for mode 1)
+ * order       int32 [n_w] device permutation of window indices: launch order
+ * m_tiles     64-row query tiles per window (ceil(max Lq / 64))
+ * H, W        token grid of the queries / HR KV
+ * scale       softmax scale applied to q.k (head_dim^-1/2 in the reference)
+ * mode        0 plain (no anchor or a whole-chunk anchor), 1 per-frame anchor
+ * dtype       SRDIT_DTYPE_BF16 or SRDIT_DTYPE_FP16
+ * Token indices computed from the table are clamped into the tensors, so a
+ * malformed table gives wrong numbers, never an out-of-bounds access.
+ */
+int srdit_window_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                          const int32_t* params, const int32_t* order,
+                          int n_w, int m_tiles, int p_stride, int hr_base,
+                          int H, int W, int64_t q_tokens, int64_t kv_tokens,
+                          int n_heads, int head_dim, float scale, int mode,
+                          int dtype, void* stream);
+
+/*
+ * Row-wise fp8 e4m3 quantiser: for each row of x [M, K] (bf16),
+ *   scale[m] = max(amax(|x[m,:]|) / 448, 1e-12);  xq = e4m3(clamp(x / scale, +-448))
+ * with round-to-nearest-even.  Replaces _quantize_rowwise_impl
+ * (video_refiner/wan/modules/sr_dit/fp8_linear.py:93-103).
+ * xq [M, K] uint8 (OCP e4m3fn bytes), scale [M] float.
+ */
+int srdit_fp8_quant_rowwise(const void* x, int64_t M, int64_t K, int64_t ldx,
+                            void* xq, float* scale, void* stream);
+
+/*
+ * Per-tensor fp8 e4m3 quantiser, two launches on `stream`:
+ * amax over all of x [M, K] (bf16) into amax_ws (one float, device; cleared by
+ * the call), then scale[0] = max(amax / 448, 1e-12) and xq = e4m3(x / scale).
+ * The per-tensor mode of the fp8 Linear; the reference quantises row-wise only
+ * (fp8_linear.py:93-103) and names per-tensor as its faster alternative
+ * (fp8_linear.py:22, :31-38).
+ */
+int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64_t ldx,
+                           void* xq, float* scale, float* amax_ws, void* stream);
+
+/*
+ * Scaled fp8 GEMM:  out[m, n] = bf16( sum_k a[m,k] b[n,k] * sa[m or 0] * sb[n or 0]
+ *                                     + bias[n] )
+ * a [M, K] e4m3 row-major, b [N, K] e4m3 row-major (the nn.Linear weight
+ * layout), fp32 accumulate, bias bf16 [N] or NULL, out bf16 [M, N] with row
+ * stride ldo.  sa_rows is 1 (per-tensor) or M (row-wise); sb_cols is 1 or N.
+ * Replaces torch._scaled_mm(xq, w_fp8.t(), scale_a, scale_b, bias,
+ * out_dtype=bf16) in Fp8Linear.forward (fp8_linear.py:282-297).
+ * Requires K % 128 == 0.
+ */
+int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_rows,
+                   const float* sb, int64_t sb_cols, const void* bias, void* out,
+                   int64_t M, int64_t N, int64_t K, int64_t ldo, void* stream);
+
+/* Message of the last failed call on this thread (NUL-terminated, truncated to
+ * len).  Returns the message length. */
+int srdit_last_error(char* buf, int len);
+
+/* Library version, packed as major*10000 + minor*100 + patch. */
+int srdit_version(void);
+
+/*
+ * Measurement helper with no counterpart in the reference: copies `bytes`
+ * (a multiple of 16) from src to dst with 16-byte vector loads and stores.
+ * Used to calibrate hardware byte counters against a kernel of known traffic.
+ */
+int srdit_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SRDIT_HIP_H */

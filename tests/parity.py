@@ -1,0 +1,62 @@
+"""Parity metrics for floating-point outputs.
+
+The stated window-attention bar is max-abs <= 2e-2 and mean-abs <= 2e-3 against
+an fp32 reference.  At the benchmark input distribution (Q/K/V ~ N(0,1)/sqrt(128))
+softmax is nearly uniform and outputs are ~2e-3 in magnitude, so an all-zero
+output would pass that bar.  Every attention check therefore also bounds the
+relative L2 error and the worst per-row relative error, which an all-zero or a
+uniform-average output fails (see tests/test_oracle.py negative controls).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+# bf16 has 8 significant bits; the kernel rounds P and O to bf16 once each,
+# which gives a relative L2 error near 1.5e-3 against an fp32 reference.  A
+# uniform average of V (softmax ignored) measures ~7.7e-3 at the benchmark
+# distribution, so 4e-3 separates the two with a 2x margin on both sides.
+REL_L2 = 4e-3
+ROW_REL = 2e-2
+
+
+def _np(x):
+    if torch.is_tensor(x):
+        return x.detach().float().cpu().numpy().astype(np.float64)
+    return np.asarray(x, dtype=np.float64)
+
+
+def metrics(out, ref):
+    o, r = _np(out), _np(ref)
+    err = np.abs(o - r)
+    rows_o = o.reshape(-1, o.shape[-1])
+    rows_r = r.reshape(-1, r.shape[-1])
+    row_err = np.linalg.norm(rows_o - rows_r, axis=1) / np.maximum(np.linalg.norm(rows_r, axis=1), 1e-30)
+    return {
+        "max_abs": float(err.max()),
+        "mean_abs": float(err.mean()),
+        "rel_l2": float(np.linalg.norm(o - r) / max(np.linalg.norm(r), 1e-30)),
+        "row_rel_max": float(row_err.max()),
+        "finite": bool(np.isfinite(o).all()),
+    }
+
+
+def check_attention(out, ref, *, rel_l2=REL_L2, row_rel=ROW_REL, label=""):
+    m = metrics(out, ref)
+    ok = (m["finite"] and m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS
+          and m["rel_l2"] <= rel_l2 and m["row_rel_max"] <= row_rel)
+    assert ok, f"{label} parity failed: {m}"
+    return m
+
+
+def passes_attention(out, ref, *, rel_l2=REL_L2, row_rel=ROW_REL):
+    m = metrics(out, ref)
+    return (m["finite"] and m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS
+            and m["rel_l2"] <= rel_l2 and m["row_rel_max"] <= row_rel)
+
+
+def passes_baseline_tolerance_only(out, ref):
+    m = metrics(out, ref)
+    return m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS
