@@ -1,0 +1,217 @@
+"""Benchmark: block-grid window attention at 2K (6x45x80 = 21,600 tokens, 24x128, bf16).
+
+One step = one window-attention layer forward over the full 2K latent (the
+fused HIP kernel, one launch), inputs resident in HBM.  Reports useful TFLOP/s
+(sum over windows and heads of 4*Lq*Lkv*d) and the fraction of MI355X dense
+bf16 MFMA peak, plus the reference's gather path restated in torch, timed on
+the host CPU over a bounded sample, as a baseline only.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c3]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import re
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "dreamx-creator_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, spec sheet
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, spec sheet
+CONFIG_DESC = {
+    "c2": "window attention 1080p latent 6x34x60 (12,240 tok), 24 heads x 128, 8x8 blocks, 3x3 nbhd, +-1 frame",
+    "c3": "window attention 2K latent 6x45x80 (21,600 tok), 24 heads x 128, 8x8 blocks, 3x3 nbhd, +-1 frame",
+    "c4": "AR window attention: 2x45x80 query frames vs 4 cached + 2 current frames, 24 heads x 128, 8x8 blocks, 3x3 nbhd",
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIG_DESC))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="rough budget for the CPU baseline sample")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run the library's 16-byte copy kernel over BYTES (counter calibration)")
+    return ap.parse_args()
+
+
+def copy_calibration(nbytes, reps=5):
+    """Launch the plain copy kernel `reps` times over `nbytes`: a kernel of known traffic
+    (nbytes read + nbytes written per launch) to scale hardware byte counters against."""
+    import torch
+    from sr_dit import _lib
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        _lib.copy_bytes(src, dst, nbytes)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "launches": reps}), flush=True)
+
+
+def profile_traffic(config):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+    path = os.path.join(ROOT, "profiles", f"window_attn_{config}_pmc.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(config, budget_s):
+    """The oracle's torch gather path (fp32) on the host cores, bounded sample.
+
+    Sample: the windows of one interior query frame (frame 2: 60 windows of the
+    6x45x80 grid), all 24 heads, fp32, same seeded inputs.  3 warm-up runs, then
+    the median of up to 10 timed runs within the budget.
+    """
+    import torch
+    from oracle import blockgrid as obg
+    from oracle import gather_torch as ogt
+    from sr_dit import workloads as wl
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    c = wl.WINDOW_CONFIGS[config]
+    q, k, v, kc, vc = wl.make_window_inputs(config, torch.float32, "cpu", seed=0)
+    q, k, v = q[0], k[0], v[0]
+    if kc is not None:
+        k, v = torch.cat([kc[0], k]), torch.cat([vc[0], v])
+    spec = wl.window_spec(config)
+    g = obg.Geometry(**{f: getattr(spec, f) for f in obg.Geometry.__dataclass_fields__})
+    wins = obg.windows(g)
+    L = c["h"] * c["w"]
+    frame = min(2, c["f_cur"] - 1)
+    sample = [w for w in wins if w[0][0] // L == frame] if c["rule"] == "sym1" else wins[:12]
+    flops = sum(4 * len(a) * len(b) * wl.HEAD_DIM for a, b in sample) * wl.N_HEADS
+    plan = ogt.GatherPlan(g)
+    # restrict the plan to the sample windows
+    keep = {int(a[0]) for a, _ in sample}
+    groups = []
+    for grp in plan.groups:
+        qs = grp["q"].view(grp["Nw"], grp["Lq"])
+        kvs = grp["kv"].view(grp["Nw"], grp["Lkv"])
+        sel = [i for i in range(grp["Nw"]) if int(qs[i, 0]) in keep]
+        if sel:
+            groups.append({"q": qs[sel].reshape(-1), "kv": kvs[sel].reshape(-1), "Nw": len(sel),
+                           "Lq": grp["Lq"], "Lkv": grp["Lkv"]})
+    plan.groups = groups
+    times = []
+    t_start = time.perf_counter()
+    for i in range(13):
+        t0 = time.perf_counter()
+        ogt.gather_attend(plan, q, k, v)
+        dt = time.perf_counter() - t0
+        if i >= 3:
+            times.append(dt)
+        if time.perf_counter() - t_start > budget_s and len(times) >= 3:
+            break
+    med = statistics.median(times)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        cpu_model = platform.processor()
+    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"{config} query frame {frame}: {len(sample)} windows x 24 heads, fp32, "
+                       f"{flops / 1e9:.2f} GFLOP useful, median of {len(times)} runs "
+                       f"{med * 1e3:.1f} ms; os.cpu_count()={os.cpu_count()}; {cpu_model}")}
+
+
+def main():
+    args = parse()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the window attention "
+              "and fp8 paths have no multi-GPU implementation here.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from sr_dit import blockgrid_hip as bgh
+    from sr_dit import workloads as wl
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    cfg = args.config
+    spec = wl.window_spec(cfg)
+    plan = bgh.build_plan(spec)
+    q, k, v, kc, vc = wl.make_window_inputs(cfg, torch.bfloat16, dev, seed=0)
+    q, k, v = q[0].contiguous(), k[0], v[0]
+    if kc is not None:
+        k, v = torch.cat([kc[0], k]), torch.cat([vc[0], v])
+    k, v = k.contiguous(), v.contiguous()
+    out = torch.empty_like(q)
+    n, d = wl.N_HEADS, wl.HEAD_DIM
+
+    def step():
+        bgh.run_blockgrid_hip(q, k, v, out, plan=plan, f_cur=spec.f_cur, h=spec.h, w=spec.w,
+                              n=n, d=d)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+
+    flops = wl.plan_useful_flops(plan)
+    tflops = flops / (ms * 1e-3) / 1e12
+    s_q = q.shape[0]
+    s_kv = k.shape[0]
+    alg_bytes = (2 * s_q + 2 * s_kv) * n * d * 2      # Q + O + K + V once, bf16
+    traffic = profile_traffic(cfg)
+    result = {
+        "metric": "window-attn TFLOP/s & % MFMA peak @2K (21.6k tok); ms per SR-DiT 5B step",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)/sqrt(128) Q/K/V, generated on the CPU)",
+        "config": {"workload": CONFIG_DESC[cfg], "tokens": s_q, "kv_tokens": s_kv,
+                   "heads": n, "head_dim": d, "windows": plan["n_w"],
+                   "useful_gflop": round(flops / 1e9, 2), "parallelism": "single GPU"},
+        "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic,
+                     "algorithmic_bytes": alg_bytes,
+                     "algorithmic_hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1)},
+        "wall_s_timed_region": round(wall, 4),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -94,6 +94,8 @@ __device__ __forceinline__ float half_sum(float x) {
 }
 
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
 
 // One contiguous run of keys with a common decode.
 //   kind 0: HR cuboid   flat = base + (t0 + j/sp)*L + (r0 + (j%sp)/cw)*Wg + c0 + (j%sp)%cw
@@ -143,6 +145,11 @@ struct Tile {
   float mrun[QT], lrun[QT];
 };
 
+// Largest growth (log2 units) of a query's running max tolerated before the
+// accumulator is rescaled.  Between rescales P = exp2(s - m_used) <= 2^TAU, which
+// the final O = acc / l normalisation cancels exactly; it only bounds the range.
+constexpr float TAU = 8.0f;
+
 // Walk one key run: online softmax over 32-key steps.  `seg` >= 0 restricts
 // the run to queries of frame `seg` (per-frame anchor), -1 admits all.
 template <typename T, int D>
@@ -158,6 +165,7 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
   if (run.n <= 0) return;
   const int lane = threadIdx.x;
   const int c = lane & 31, hf = lane >> 5;
+  const int g = lane >> 4, i16 = lane & 15;
 
   bool admit[QT];
 #pragma unroll
@@ -170,36 +178,32 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
     if (!__any(any)) return;
   }
 
-  auto load_kv = [&](int s0, V8 (&kf)[KS], V8 (&vf)[KS]) {
+  // Per step: K (32 keys) goes straight to registers as the MFMA A operand,
+  // lane (c, hf) holding key c, head dims [hf*HD, hf*HD + HD).  V goes straight
+  // to LDS with global_load_lds_dwordx4 (no registers): load q of a step places
+  // lane l's 16 bytes at slot 64q + l, i.e. chunk L = 2q + hf (8 head dims) of
+  // key c ^ (8 * hf).  So slot = L*32 + (key ^ 8*(L & 1)): the eight keys x four
+  // chunks a transposing read touches land on distinct bank groups.
+  auto load_k = [&](int s0, V8 (&kf)[KS]) {
     const int j = s0 + c;
-    const bool ok = j < run.n;
-    int64_t flat = run_token(run, ok ? j : run.n - 1);
+    int64_t flat = run_token(run, j < run.n ? j : run.n - 1);
     flat = flat < 0 ? 0 : (flat >= kv_tokens ? kv_tokens - 1 : flat);
     const V8* kp = reinterpret_cast<const V8*>(kb + flat * tok + hf * HD);
-    const V8* vp = reinterpret_cast<const V8*>(vb + flat * tok + hf * HD);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = kp[ks];
-      vf[ks] = vp[ks];
-    }
-    if (!ok) {
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = kp[ks];
+  };
+  auto load_v = [&](int s0, T* buf) {
+    const int j = s0 + (c ^ (8 * hf));
+    int64_t flat = run_token(run, j < run.n ? j : run.n - 1);
+    flat = flat < 0 ? 0 : (flat >= kv_tokens ? kv_tokens - 1 : flat);
+    const T* vp = vb + flat * tok + hf * 8;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) vf[ks] = V8{};
-    }
+    for (int q = 0; q < D / 16; ++q)
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(const_cast<T*>(vp + q * 16)),
+                                       (lds_void_t*)(buf + q * 512), 16, 0, 0);
   };
 
-  V8 kcur[KS], vcur[KS];
-  load_kv(0, kcur, vcur);
-  for (int s0 = 0; s0 < run.n; s0 += KN) {
-    V8 knext[KS], vnext[KS];
-    const bool more = s0 + KN < run.n;
-    if (more) load_kv(s0 + KN, knext, vnext);
-
-    // stage V: lane (c, hf) holds key c, head dims [hf*HD, hf*HD + HD)
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      *reinterpret_cast<V8*>(vsh + c * VS + hf * HD + ks * 8) = vcur[ks];
-
+  auto step = [&](int s0, const V8 (&kcur)[KS], const T* vbuf) {
     // S^T = K . Q^T
     f32x16_t sacc[QT];
 #pragma unroll
@@ -209,52 +213,63 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) sacc[qt] = E::mma(kcur[ks], st.qf[qt][ks], sacc[qt]);
 
-    // online softmax, one query per lane
-    V8 pf[QT][2];
+    // Masking is needed only on a partial last step or inside an anchor segment.
     const int nvalid = run.n - s0;
+    if (nvalid < KN || seg >= 0) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = 8 * (r >> 2) + 4 * hf + (r & 3);
+          if (!(key < nvalid && admit[qt])) sacc[qt][r] = -INFINITY;
+        }
+    }
+
+    // online softmax, one query per lane, lazily rescaled
+    V8 pf[QT][2];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      float sv[16];
-      float mx = -INFINITY;
+      float mx = sacc[qt][0];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = 8 * (r >> 2) + 4 * hf + (r & 3);
-        sv[r] = (key < nvalid && admit[qt]) ? sacc[qt][r] * scale_log2 : -INFINITY;
-        mx = fmaxf(mx, sv[r]);
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[qt][r]);
+      mx = other_half_max(mx) * scale_log2;
+      // A lane rescales when its max grew by more than TAU (mx is then finite);
+      // lanes with a fully masked tile (mx = -inf) never do.
+      const bool up = mx > st.mrun[qt] + TAU;
+      if (__any(up)) {
+        const float alpha = up ? __builtin_amdgcn_exp2f(st.mrun[qt] - mx) : 1.0f;  // 0 on a first tile
+        st.lrun[qt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) st.oacc[qt][dt] *= alpha;
+        st.mrun[qt] = up ? mx : st.mrun[qt];
       }
-      mx = other_half_max(mx);
-      const float mnew = fmaxf(st.mrun[qt], mx);
-      const bool live = mnew != -INFINITY;
-      const float alpha = live ? __builtin_amdgcn_exp2f(st.mrun[qt] - mnew) : 1.0f;
-      float psum = 0.f;
+      // Until the first unmasked score the running max is -inf and every P is 0.
+      const float msub = st.mrun[qt] == -INFINITY ? 0.f : st.mrun[qt];
       float pv[16];
+      float psum = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        pv[r] = live ? __builtin_amdgcn_exp2f(sv[r] - mnew) : 0.f;
+        pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qt][r], scale_log2, -msub));
         psum += pv[r];
       }
-      st.lrun[qt] = st.lrun[qt] * alpha + psum;
-      st.mrun[qt] = mnew;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) st.oacc[qt][dt] *= alpha;
+      st.lrun[qt] += psum;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) pf[qt][kk] = E::pack8(&pv[kk * 8]);
     }
 
-    __syncthreads();  // staged V visible to every lane
-
     // O^T += V^T . P^T ; V^T operand via transposing LDS reads
-    const int g = lane >> 4, i16 = lane & 15;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const int dimbase = dt * 32 + 16 * (g & 1);
+        // lane reads 8 bytes of chunk L = 4dt + 2(g&1) + (i16&3)/2, half (i16&1),
+        // of key keybase + i16/4
+        const int L = 4 * dt + 2 * (g & 1) + ((i16 & 3) >> 1);
         i32x2_t half[2];
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
-          const int keybase = 16 * kk + 8 * h2 + 4 * hf;
-          const T* src = vsh + (keybase + (i16 >> 2)) * VS + dimbase + 4 * (i16 & 3);
+          const int key = 16 * kk + 8 * h2 + 4 * hf + (i16 >> 2);
+          const T* src = vbuf + (L * 32 + (key ^ (8 * (L & 1)))) * 8 + 4 * (i16 & 1);
           half[h2] = __builtin_bit_cast(
               i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(const_cast<T*>(src))));
         }
@@ -264,15 +279,36 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
         for (int qt = 0; qt < QT; ++qt) st.oacc[qt][dt] = E::mma(vt, pf[qt][kk], st.oacc[qt][dt]);
       }
     }
-    __syncthreads();  // reads done before the next step restages V
+  };
 
-    if (more) {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        kcur[ks] = knext[ks];
-        vcur[ks] = vnext[ks];
-      }
+  // Step i's K (registers) and V (LDS buffer i % 2) are loaded during step i-1.
+  // At the top of each step: wait for them, make the LDS writes visible, then
+  // issue step i+1's loads.  The barrier at the end of a step retires its LDS
+  // reads before the buffer is refilled two steps later.
+  T* vbuf0 = vsh;
+  T* vbuf1 = vsh + KN * D;
+  V8 ka[KS], kb2[KS];
+  load_k(0, ka);
+  load_v(0, vbuf0);
+  for (int s0 = 0; s0 < run.n; s0 += 2 * KN) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const bool has_b = s0 + KN < run.n;
+    if (has_b) {
+      load_k(s0 + KN, kb2);
+      load_v(s0 + KN, vbuf1);
     }
+    step(s0, ka, vbuf0);
+    __syncthreads();
+    if (!has_b) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (s0 + 2 * KN < run.n) {
+      load_k(s0 + 2 * KN, ka);
+      load_v(s0 + 2 * KN, vbuf0);
+    }
+    step(s0 + KN, kb2, vbuf1);
+    __syncthreads();
   }
 }
 
@@ -282,16 +318,19 @@ __global__ __launch_bounds__(64) void window_attn_kernel(WinArgs a) {
   using E = typename TT::E;
   using V8 = typename TT::V8;
   constexpr int KS = TT::KS, DT = TT::DT, VS = TT::VS, HD = TT::HD;
-  __shared__ __attribute__((aligned(16))) T vsh[KN * VS];
+  __shared__ __attribute__((aligned(16))) T vsh[2 * KN * D];
 
   const int lane = threadIdx.x;
   const int c = lane & 31, hf = lane >> 5;
   const uint32_t task = xcd_task(blockIdx.x, gridDim.x);
-  const int head = static_cast<int>(task % static_cast<uint32_t>(a.n_heads));
-  const uint32_t rest = task / static_cast<uint32_t>(a.n_heads);
+  // Head-major: each XCD walks whole heads, so the waves sharing its L2 read
+  // overlapping KV cuboids of one head.
+  const uint32_t per_head = static_cast<uint32_t>(a.n_w) * static_cast<uint32_t>(a.m_tiles);
+  const int head = static_cast<int>(task / per_head);
+  const uint32_t rest = task % per_head;
   const int mt = static_cast<int>(rest % static_cast<uint32_t>(a.m_tiles));
   const uint32_t wslot = rest / static_cast<uint32_t>(a.m_tiles);
-  if (wslot >= static_cast<uint32_t>(a.n_w)) return;
+  if (wslot >= static_cast<uint32_t>(a.n_w) || head >= a.n_heads) return;
   int wid = a.order[wslot];
   wid = wid < 0 ? 0 : (wid >= a.n_w ? a.n_w - 1 : wid);
   const int32_t* p = a.params + static_cast<int64_t>(wid) * a.p_stride;
