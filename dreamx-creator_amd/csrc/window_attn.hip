@@ -1,7 +1,8 @@
 // Block-grid window attention forward for gfx950 (MI355X).
 //
-// One wavefront owns one task = (window, 64-query tile, head).  It walks the
-// window's KV cuboid 32 keys per step with an online softmax:
+// One workgroup of two wavefronts owns one task = (window, 64-query tile,
+// head); wavefront w owns queries [32w, 32w + 32) of the tile.  The workgroup
+// walks the window's KV cuboid 32 keys per step with an online softmax:
 //
 //   S^T[32 keys x 32 queries] = K[32 x D] . Q^T[D x 32]      (v_mfma 32x32x16)
 //   O^T[D x 32 queries]      += V^T[D x 32 keys] . P^T[32 x 32]
@@ -10,25 +11,46 @@
 // softmax statistics are lane-local: a lane and its partner lane+32 hold the
 // same query's 16+16 keys, and one permlane32 swap combines them.  The S^T
 // accumulator registers feed the P^T operand of the second MFMA directly (the
-// contraction over keys uses the accumulator's own key order), and V^T comes
-// out of LDS with ds_read_b64_tr_b16, so no shuffles are needed anywhere.
+// contraction over keys uses the accumulator's own key order).
+//
+// K and V tiles of a step are fetched once per workgroup straight into LDS
+// with global_load_lds_dwordx4 (wavefront 0 fetches K, wavefront 1 fetches V)
+// into two-stage rings, so the fetch of step i+1 overlaps step i.  K is read
+// back as the MFMA A operand with ds_read_b128, V^T with ds_read_b64_tr_b16.
+// Two wavefronts per SIMD keep the matrix pipe busy while the other one runs
+// its softmax.
 //
 // Semantics follow the reference kernels
 // (video_refiner/wan/modules/sr_dit/blockgrid_triton.py:184-278 plain,
 //  :281-389 per-frame anchor): scale applied to q.k in fp32, masked keys never
 // contribute, a fully masked tile leaves the running statistics unchanged,
 // P is rounded to the input dtype before P.V, fp32 accumulation, O = acc / l.
-// The exponential is evaluated as exp2 of log2(e)-scaled logits.
+// The exponential is evaluated as exp2 of log2(e)-scaled logits, and the
+// running max is refreshed lazily (see TAU).
 
 #include "common.h"
+
+#include <utility>
 
 namespace srdit {
 namespace {
 
-template <typename T> struct Elem;
+// Unrolled loop with a compile-time index (DPP controls must be immediates).
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
 
 // Eight fp32 values -> one 8-element MFMA operand, converted two at a time
 // (v_cvt_pk_*) and assembled as whole 32-bit registers.
@@ -43,13 +65,14 @@ __device__ __forceinline__ V8 pack8_impl(const float* x) {
   return __builtin_bit_cast(V8, w);
 }
 
+template <typename T> struct Elem;
 template <> struct Elem<__bf16> {
   typedef bf16x8_t v8;
   typedef bf16x2_t h2;
   static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<bf16x2_t, v8>(x); }
+  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<h2, v8>(x); }
 };
 template <> struct Elem<_Float16> {
   typedef f16x8_t v8;
@@ -57,7 +80,7 @@ template <> struct Elem<_Float16> {
   static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<f16x2_t, v8>(x); }
+  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<h2, v8>(x); }
 };
 
 struct WinArgs {
@@ -73,8 +96,14 @@ struct WinArgs {
   float scale_log2;  // softmax scale * log2(e)
 };
 
-constexpr int QT = 2;   // 32-query MFMA tiles per wavefront
-constexpr int KN = 32;  // keys per step
+constexpr int WAVES = 2;  // wavefronts per workgroup, 32 queries each
+constexpr int KN = 32;    // keys per step
+
+// Largest growth (log2 units) of a query's running max tolerated before the
+// accumulator is rescaled.  Between rescales P = exp2(s - m_used) <= 2^TAU,
+// which the final O = acc / l normalisation cancels exactly; it only bounds
+// the range (2^8 fits bf16 and fp16 P with room to spare).
+constexpr float TAU = 8.0f;
 
 // n / d for 0 <= n < 2^22, d > 0, rd = 1/d: float estimate plus one correction.
 __device__ __forceinline__ int fdiv(int n, int d, float rd) {
@@ -93,14 +122,24 @@ __device__ __forceinline__ float half_sum(float x) {
   return __int_as_float(s[0]) + __int_as_float(s[1]);
 }
 
-typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
+// Compiler-only fence: keeps LDS/DMA accesses on their side of a wait or a
+// barrier without emitting any wait of its own.
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
-// One contiguous run of keys with a common decode.
-//   kind 0: HR cuboid   flat = base + (t0 + j/sp)*L + (r0 + (j%sp)/cw)*Wg + c0 + (j%sp)%cw
-//   the anchor prefix of the plain kernel and an anchor segment of the frame
-//   kernel are the same formula with their own grid and a frame base.
+// All of this wavefront's memory operations (the DMA fills, the LDS reads)
+// retired, then a workgroup barrier: after it every fill issued before it by
+// either wavefront is in LDS, and every LDS read issued before it has returned.
+__device__ __forceinline__ void fill_barrier() {
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  compiler_fence();
+}
+
+// One contiguous run of keys with a common decode:
+//   token = base + (t0 + j/sp)*frame_len + (r0 + (j%sp)/cols)*Wg + c0 + (j%sp)%cols
+// The HR cuboid, the anchor prefix of the plain kernel and an anchor segment of
+// the frame kernel are all this formula with their own grid.
 struct KeyRun {
   int n;          // keys in the run
   int64_t base;   // token offset of frame 0 of the run
@@ -137,194 +176,176 @@ struct Tile {
   using V8 = typename E::v8;
   static constexpr int KS = D / 16;  // k-steps of the S^T MFMA over the head dim
   static constexpr int DT = D / 32;  // 32-row tiles of O^T over the head dim
-  static constexpr int VS = D + 8;   // LDS row stride of the staged V tile (elements)
-  static constexpr int HD = D / 2;   // head-dim elements per lane half
+  static constexpr int NL = D / 16;  // 16-byte fill loads per lane per tile
 
-  V8 qf[QT][KS];
-  f32x16_t oacc[QT][DT];
-  float mrun[QT], lrun[QT];
+  V8 qf[KS];           // Q^T operand: lane (c, hf), k-step ks -> dims [hf*D/2 + 8ks, +8)
+  f32x16_t oacc[DT];   // O^T accumulator, rows = head dims, column = query c
+  float mrun, lrun;    // running max (log2 units, lazily refreshed) and sum
 };
 
-// Largest growth (log2 units) of a query's running max tolerated before the
-// accumulator is rescaled.  Between rescales P = exp2(s - m_used) <= 2^TAU, which
-// the final O = acc / l normalisation cancels exactly; it only bounds the range.
-constexpr float TAU = 8.0f;
-
-// Walk one key run: online softmax over 32-key steps.  `seg` >= 0 restricts
-// the run to queries of frame `seg` (per-frame anchor), -1 admits all.
+// Walk one key run with the online softmax.  `seg` >= 0 restricts the run to
+// queries of frame `seg` (per-frame anchor), -1 admits all.  Must be called
+// by both wavefronts of the workgroup with the same run (barriers inside).
+//
+// LDS tiles: 32 keys x D, one row of CPK 16-byte slots per key (chunk L = 8
+// head dims), row-major with an XOR swizzle of the slot within its row:
+//   slot(key, L) = key*CPK + (L ^ swz(key)).
+// Fill load q writes slots [64q, 64q + 64): lane l covers key 64q+l / CPK at
+// row position l % CPK, i.e. CPK consecutive lanes read one key's whole
+// contiguous head row (chunk (l % CPK) ^ swz(key)), so each load touches
+// 64/CPK full rows.  The swizzles (K: (key*CPK/16) % CPK; V: for D=128
+// 4(key%4) ^ 8((key>>2)&1), for D=64 key%8) make the K A-operand reads and the
+// V transposing reads hit every bank group equally often.
 template <typename T, int D>
-__device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, int seg,
-                                           const int (&qframe)[QT], const bool (&qvalid)[QT],
+__device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, int seg, int wave,
+                                           int qframe, bool qvalid,
                                            const T* __restrict__ kb, const T* __restrict__ vb,
                                            int64_t tok, int64_t kv_tokens, float scale_log2,
-                                           T* vsh) {
+                                           T* ksh, T* vsh) {
   using TT = Tile<T, D>;
   using E = typename TT::E;
   using V8 = typename TT::V8;
-  constexpr int KS = TT::KS, DT = TT::DT, VS = TT::VS, HD = TT::HD;
+  constexpr int KS = TT::KS, DT = TT::DT, NL = TT::NL;
+  constexpr int TILE = KN * D;  // elements per LDS stage
+  constexpr int CPK = D / 8;    // 16-byte chunks per key row
+  constexpr int LPK = CPK;      // fill lanes per key row
+  constexpr int KPI = 64 / CPK; // key rows per fill load
+  auto swz_k = [](int key) { return (key * CPK / 16) % CPK; };
+  auto swz_v = [](int key) {
+    return D == 128 ? ((4 * (key & 3)) ^ (8 * ((key >> 2) & 1))) : (key % CPK);
+  };
   if (run.n <= 0) return;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int c = lane & 31, hf = lane >> 5;
   const int g = lane >> 4, i16 = lane & 15;
+  const int nsteps = (run.n + KN - 1) / KN;
+  const bool admit = (seg < 0) || (qvalid && qframe == seg);
 
-  bool admit[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) admit[qt] = (seg < 0) || (qvalid[qt] && qframe[qt] == seg);
-  if (seg >= 0) {
-    // Skip the run if no query of this tile belongs to the segment.
-    bool any = false;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) any |= admit[qt];
-    if (!__any(any)) return;
-  }
-
-  // Per step: K (32 keys) goes straight to registers as the MFMA A operand,
-  // lane (c, hf) holding key c, head dims [hf*HD, hf*HD + HD).  V goes straight
-  // to LDS with global_load_lds_dwordx4 (no registers): load q of a step places
-  // lane l's 16 bytes at slot 64q + l, i.e. chunk L = 2q + hf (8 head dims) of
-  // key c ^ (8 * hf).  So slot = L*32 + (key ^ 8*(L & 1)): the eight keys x four
-  // chunks a transposing read touches land on distinct bank groups.
-  auto load_k = [&](int s0, V8 (&kf)[KS]) {
-    const int j = s0 + c;
+  // Fill of step i into stage i & 1: wavefront 0 loads K, wavefront 1 loads V.
+  // The token of each key row is decoded once per step by a source lane and
+  // broadcast to the row's lanes with DPP row_newbcast: source lane s of a
+  // 16-lane row r holds the key that load (s % LPK) places in that row's
+  // sub-row s / LPK.
+  auto fill = [&](int i) {
+    const int s = lane & 15;
+    const int src_key = (s % LPK) * KPI + (lane >> 4) * (16 / LPK) + s / LPK;
+    const int j = i * KN + src_key;
     int64_t flat = run_token(run, j < run.n ? j : run.n - 1);
-    flat = flat < 0 ? 0 : (flat >= kv_tokens ? kv_tokens - 1 : flat);
-    const V8* kp = reinterpret_cast<const V8*>(kb + flat * tok + hf * HD);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = kp[ks];
-  };
-  auto load_v = [&](int s0, T* buf) {
-    const int j = s0 + (c ^ (8 * hf));
-    int64_t flat = run_token(run, j < run.n ? j : run.n - 1);
-    flat = flat < 0 ? 0 : (flat >= kv_tokens ? kv_tokens - 1 : flat);
-    const T* vp = vb + flat * tok + hf * 8;
-#pragma unroll
-    for (int q = 0; q < D / 16; ++q)
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(const_cast<T*>(vp + q * 16)),
-                                       (lds_void_t*)(buf + q * 512), 16, 0, 0);
+    const int tokv = static_cast<int>(flat < 0 ? 0 : (flat >= kv_tokens ? kv_tokens - 1 : flat));
+    const T* base = wave == 0 ? kb : vb;
+    T* dst = (wave == 0 ? ksh : vsh) + (i & 1) * TILE;
+    const int sub = s / LPK, pos = lane % CPK;
+    static_for<NL>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      int t = __builtin_amdgcn_mov_dpp(tokv, 0x150 + q, 0xf, 0xf, false);
+      if constexpr (LPK == 8) {
+        const int t1 = __builtin_amdgcn_mov_dpp(tokv, 0x150 + 8 + q, 0xf, 0xf, false);
+        t = sub ? t1 : t;
+      }
+      const int key = q * KPI + (lane >> 4) * (16 / LPK) + sub;
+      const int chunk = pos ^ (wave == 0 ? swz_k(key) : swz_v(key));
+      const T* src = base + static_cast<int64_t>(t) * tok + chunk * 8;
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(const_cast<T*>(src)),
+                                       (lds_void_t*)(dst + q * 512), 16, 0, 0);
+    });
   };
 
-  auto step = [&](int s0, const V8 (&kcur)[KS], const T* vbuf) {
-    // S^T = K . Q^T
-    f32x16_t sacc[QT];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) sacc[qt] = f32x16_t{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) sacc[qt] = E::mma(kcur[ks], st.qf[qt][ks], sacc[qt]);
+  fill(0);
+  for (int i = 0; i < nsteps; ++i) {
+    // Fill i (issued one step ago) has landed in both halves, and step i-1's
+    // LDS reads are done, so stage (i+1) & 1 may be refilled.
+    fill_barrier();
+    if (i + 1 < nsteps) fill(i + 1);
+    const T* kbuf = ksh + (i & 1) * TILE;
+    const T* vbuf = vsh + (i & 1) * TILE;
 
-    // Masking is needed only on a partial last step or inside an anchor segment.
-    const int nvalid = run.n - s0;
+    // S^T = K Q^T
+    f32x16_t sacc = f32x16_t{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const V8 kf =
+          *reinterpret_cast<const V8*>(kbuf + (c * CPK + ((hf * KS + ks) ^ swz_k(c))) * 8);
+      sacc = E::mma(kf, st.qf[ks], sacc);
+    }
+
+    // masking on a partial last step or inside an anchor segment
+    const int nvalid = run.n - i * KN;
     if (nvalid < KN || seg >= 0) {
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = 8 * (r >> 2) + 4 * hf + (r & 3);
-          if (!(key < nvalid && admit[qt])) sacc[qt][r] = -INFINITY;
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int key = 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (!(key < nvalid && admit)) sacc[r] = -INFINITY;
+      }
     }
 
     // online softmax, one query per lane, lazily rescaled
-    V8 pf[QT][2];
+    float mx = sacc[0];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      float mx = sacc[qt][0];
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
+    mx = other_half_max(mx) * scale_log2;
+    // A lane rescales when its max grew by more than TAU (mx is then finite);
+    // a lane with a fully masked tile (mx = -inf) never does.
+    const bool up = mx > st.mrun + TAU;
+    if (__any(up)) {
+      const float alpha = up ? __builtin_amdgcn_exp2f(st.mrun - mx) : 1.0f;  // 0 on a first tile
+      st.lrun *= alpha;
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[qt][r]);
-      mx = other_half_max(mx) * scale_log2;
-      // A lane rescales when its max grew by more than TAU (mx is then finite);
-      // lanes with a fully masked tile (mx = -inf) never do.
-      const bool up = mx > st.mrun[qt] + TAU;
-      if (__any(up)) {
-        const float alpha = up ? __builtin_amdgcn_exp2f(st.mrun[qt] - mx) : 1.0f;  // 0 on a first tile
-        st.lrun[qt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) st.oacc[qt][dt] *= alpha;
-        st.mrun[qt] = up ? mx : st.mrun[qt];
-      }
-      // Until the first unmasked score the running max is -inf and every P is 0.
-      const float msub = st.mrun[qt] == -INFINITY ? 0.f : st.mrun[qt];
-      float pv[16];
-      float psum = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qt][r], scale_log2, -msub));
-        psum += pv[r];
-      }
-      st.lrun[qt] += psum;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) pf[qt][kk] = E::pack8(&pv[kk * 8]);
+      for (int dt = 0; dt < DT; ++dt) st.oacc[dt] *= alpha;
+      st.mrun = up ? mx : st.mrun;
     }
+    // until the first unmasked score the running max is -inf and every P is 0
+    const float msub = st.mrun == -INFINITY ? 0.f : st.mrun;
+    float pv[16];
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], scale_log2, -msub));
+      psum += pv[r];
+    }
+    st.lrun += psum;
+    const V8 pf0 = E::pack8(&pv[0]);
+    const V8 pf1 = E::pack8(&pv[8]);
 
-    // O^T += V^T . P^T ; V^T operand via transposing LDS reads
+    // O^T += V^T P^T, V^T via transposing LDS reads: the lane reads 8 bytes of
+    // chunk L = 4dt + 2(g&1) + (i16&3)/2, half (i16&1), of key 16kk + 8h2 +
+    // 4hf + i16/4, and receives four consecutive keys of head dim dt*32 + c.
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        // lane reads 8 bytes of chunk L = 4dt + 2(g&1) + (i16&3)/2, half (i16&1),
-        // of key keybase + i16/4
         const int L = 4 * dt + 2 * (g & 1) + ((i16 & 3) >> 1);
         i32x2_t half[2];
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
           const int key = 16 * kk + 8 * h2 + 4 * hf + (i16 >> 2);
-          const T* src = vbuf + (L * 32 + (key ^ (8 * (L & 1)))) * 8 + 4 * (i16 & 1);
+          const T* src = vbuf + (key * CPK + (L ^ swz_v(key))) * 8 + 4 * (i16 & 1);
           half[h2] = __builtin_bit_cast(
               i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(const_cast<T*>(src))));
         }
         const i32x4_t vw = {half[0][0], half[0][1], half[1][0], half[1][1]};
         const V8 vt = __builtin_bit_cast(V8, vw);
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) st.oacc[qt][dt] = E::mma(vt, pf[qt][kk], st.oacc[qt][dt]);
+        st.oacc[dt] = E::mma(vt, kk == 0 ? pf0 : pf1, st.oacc[dt]);
       }
     }
-  };
-
-  // Step i's K (registers) and V (LDS buffer i % 2) are loaded during step i-1.
-  // At the top of each step: wait for them, make the LDS writes visible, then
-  // issue step i+1's loads.  The barrier at the end of a step retires its LDS
-  // reads before the buffer is refilled two steps later.
-  T* vbuf0 = vsh;
-  T* vbuf1 = vsh + KN * D;
-  V8 ka[KS], kb2[KS];
-  load_k(0, ka);
-  load_v(0, vbuf0);
-  for (int s0 = 0; s0 < run.n; s0 += 2 * KN) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    const bool has_b = s0 + KN < run.n;
-    if (has_b) {
-      load_k(s0 + KN, kb2);
-      load_v(s0 + KN, vbuf1);
-    }
-    step(s0, ka, vbuf0);
-    __syncthreads();
-    if (!has_b) break;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (s0 + 2 * KN < run.n) {
-      load_k(s0 + 2 * KN, ka);
-      load_v(s0 + 2 * KN, vbuf0);
-    }
-    step(s0 + KN, kb2, vbuf1);
-    __syncthreads();
   }
+  fill_barrier();  // stages free for the next run
 }
 
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(64) void window_attn_kernel(WinArgs a) {
+__global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
   using TT = Tile<T, D>;
   using E = typename TT::E;
   using V8 = typename TT::V8;
-  constexpr int KS = TT::KS, DT = TT::DT, VS = TT::VS, HD = TT::HD;
+  constexpr int KS = TT::KS, DT = TT::DT;
+  __shared__ __attribute__((aligned(16))) T ksh[2 * KN * D];
   __shared__ __attribute__((aligned(16))) T vsh[2 * KN * D];
 
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int c = lane & 31, hf = lane >> 5;
   const uint32_t task = xcd_task(blockIdx.x, gridDim.x);
-  // Head-major: each XCD walks whole heads, so the waves sharing its L2 read
-  // overlapping KV cuboids of one head.
+  // Head-major: each XCD walks whole heads, so the workgroups sharing its L2
+  // read overlapping KV cuboids of one head.
   const uint32_t per_head = static_cast<uint32_t>(a.n_w) * static_cast<uint32_t>(a.m_tiles);
   const int head = static_cast<int>(task / per_head);
   const uint32_t rest = task % per_head;
@@ -351,7 +372,7 @@ __global__ __launch_bounds__(64) void window_attn_kernel(WinArgs a) {
   const int q_sp = qh_l * qw_l;
   const int lq = q_tl * q_sp;
   const int m0 = mt * 64;
-  if (q_sp <= 0 || q_tl <= 0 || m0 >= lq) return;
+  if (q_sp <= 0 || q_tl <= 0 || m0 >= lq) return;  // uniform over the workgroup
 
   const int L = a.H * a.W;
   const int64_t tok = static_cast<int64_t>(a.n_heads) * D;
@@ -360,31 +381,27 @@ __global__ __launch_bounds__(64) void window_attn_kernel(WinArgs a) {
   const T* vb = reinterpret_cast<const T*>(a.v) + head * D;
   T* ob = reinterpret_cast<T*>(a.o) + head * D;
 
+  // this lane's query: row m of the window, frame qframe of the window's frames
   TT st;
-  int64_t qflat[QT];
-  int qframe[QT];
-  bool qvalid[QT];
-  const float r_qsp = 1.0f / static_cast<float>(q_sp), r_qw = 1.0f / static_cast<float>(qw_l);
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int m = m0 + qt * 32 + c;
-    qvalid[qt] = m < lq;
-    const int mm = qvalid[qt] ? m : 0;
-    const int t = fdiv(mm, q_sp, r_qsp);
-    const int r = mm - t * q_sp;
-    const int hh = fdiv(r, qw_l, r_qw);
+  const int m = m0 + 32 * wave + c;
+  const bool qvalid = m < lq;
+  const int mm = qvalid ? m : 0;
+  const int qframe = fdiv(mm, q_sp, 1.0f / static_cast<float>(q_sp));
+  int64_t qflat;
+  {
+    const int r = mm - qframe * q_sp;
+    const int hh = fdiv(r, qw_l, 1.0f / static_cast<float>(qw_l));
     const int ww = r - hh * qw_l;
-    int64_t flat = static_cast<int64_t>(q_t0 + t) * L + static_cast<int64_t>(q_h0 + hh) * a.W + (q_w0 + ww);
-    flat = flat < 0 ? 0 : (flat >= a.q_tokens ? a.q_tokens - 1 : flat);
-    qflat[qt] = flat;
-    qframe[qt] = t;
-    const V8* qp = reinterpret_cast<const V8*>(qb + flat * tok + hf * HD);
+    qflat = static_cast<int64_t>(q_t0 + qframe) * L + static_cast<int64_t>(q_h0 + hh) * a.W +
+            (q_w0 + ww);
+    qflat = qflat < 0 ? 0 : (qflat >= a.q_tokens ? a.q_tokens - 1 : qflat);
+    const V8* qp = reinterpret_cast<const V8*>(qb + qflat * tok + hf * (D / 2));
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) st.qf[qt][ks] = qvalid[qt] ? qp[ks] : V8{};
+    for (int ks = 0; ks < KS; ++ks) st.qf[ks] = qvalid ? qp[ks] : V8{};
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) st.oacc[qt][dt] = f32x16_t{};
-    st.mrun[qt] = -INFINITY;
-    st.lrun[qt] = 0.f;
+    for (int dt = 0; dt < DT; ++dt) st.oacc[dt] = f32x16_t{};
+    st.mrun = -INFINITY;
+    st.lrun = 0.f;
   }
 
   const int sp_hr = kh_l * kw_l;
@@ -394,11 +411,13 @@ __global__ __launch_bounds__(64) void window_attn_kernel(WinArgs a) {
     // anchor prefix (a_frames whole-chunk anchor frames), then the HR cuboid
     if (a_frames > 0 && anchor_ok) {
       KeyRun ar = make_run(a_frames * sp_a, 0, h_a * w_a, 0, kh0_a, kw0_a, kh_l_a, kw_l_a, w_a);
-      attend_run<T, D>(st, ar, -1, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2, vsh);
+      attend_run<T, D>(st, ar, -1, wave, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2,
+                       ksh, vsh);
     }
     if (sp_hr > 0 && kv_tl > 0) {
       KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
-      attend_run<T, D>(st, hr, -1, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2, vsh);
+      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2,
+                       ksh, vsh);
     }
   } else {
     // per-frame anchor: query frame s sees anchor frame s only, over the
@@ -409,41 +428,40 @@ __global__ __launch_bounds__(64) void window_attn_kernel(WinArgs a) {
       for (int s = f_lo; s <= f_hi; ++s) {
         KeyRun ar = make_run(sp_a, static_cast<int64_t>(s) * h_a * w_a, h_a * w_a, 0, kh0_a, kw0_a,
                              kh_l_a, kw_l_a, w_a);
-        attend_run<T, D>(st, ar, s, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2, vsh);
+        attend_run<T, D>(st, ar, s, wave, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2,
+                         ksh, vsh);
       }
     }
     if (sp_hr > 0 && kv_tl > 0) {
       KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
-      attend_run<T, D>(st, hr, -1, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2, vsh);
+      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2,
+                       ksh, vsh);
     }
   }
 
   // O = acc / l ; lane (c, hf) writes dims dt*32 + 8*g4 + 4*hf + [0, 4)
+  const float lt = half_sum(st.lrun);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (!qvalid) return;
+  T* op = ob + qflat * tok;
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const float lt = half_sum(st.lrun[qt]);
-    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-    if (!qvalid[qt]) continue;
-    T* op = ob + qflat[qt] * tok;
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const f32x2_t lo = {st.oacc[qt][dt][g4 * 4 + 0] * inv, st.oacc[qt][dt][g4 * 4 + 1] * inv};
-        const f32x2_t hi = {st.oacc[qt][dt][g4 * 4 + 2] * inv, st.oacc[qt][dt][g4 * 4 + 3] * inv};
-        const i32x2_t w = {__builtin_bit_cast(int, __builtin_convertvector(lo, typename E::h2)),
-                           __builtin_bit_cast(int, __builtin_convertvector(hi, typename E::h2))};
-        *reinterpret_cast<i32x2_t*>(op + dt * 32 + g4 * 8 + hf * 4) = w;
-      }
-  }
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x2_t lo = {st.oacc[dt][g4 * 4 + 0] * inv, st.oacc[dt][g4 * 4 + 1] * inv};
+      const f32x2_t hi = {st.oacc[dt][g4 * 4 + 2] * inv, st.oacc[dt][g4 * 4 + 3] * inv};
+      const i32x2_t w = {__builtin_bit_cast(int, __builtin_convertvector(lo, typename E::h2)),
+                         __builtin_bit_cast(int, __builtin_convertvector(hi, typename E::h2))};
+      *reinterpret_cast<i32x2_t*>(op + dt * 32 + g4 * 8 + hf * 4) = w;
+    }
 }
 
 template <typename T, int D>
 int launch_window(const WinArgs& a, int mode, uint32_t grid, hipStream_t stream) {
   if (mode == 0)
-    hipLaunchKernelGGL((window_attn_kernel<T, D, 0>), dim3(grid), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((window_attn_kernel<T, D, 0>), dim3(grid), dim3(64 * WAVES), 0, stream, a);
   else
-    hipLaunchKernelGGL((window_attn_kernel<T, D, 1>), dim3(grid), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((window_attn_kernel<T, D, 1>), dim3(grid), dim3(64 * WAVES), 0, stream, a);
   SRDIT_LAUNCH_CHECK("window_attn_kernel");
   return SRDIT_OK;
 }
@@ -469,7 +487,7 @@ extern "C" int srdit_window_attn_fwd(const void* q, const void* k, const void* v
                 n_w, m_tiles, n_heads, H, W, hr_base);
   SRDIT_REQUIRE(q_tokens >= 1 && kv_tokens >= 1 && q_tokens < (1LL << 31) && kv_tokens < (1LL << 31),
                 "srdit_window_attn_fwd: token counts out of range");
-  SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 30), "srdit_window_attn_fwd: grid too large");
+  SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 22), "srdit_window_attn_fwd: grid too large");
   if (head_dim != 64 && head_dim != 128) {
     set_error("srdit_window_attn_fwd: head_dim %d unsupported (64 or 128)", head_dim);
     return SRDIT_EUNSUPPORTED;

@@ -20,9 +20,12 @@ INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(PKG_DIR, "libsrdit_hip.so")
 
 ARCH = "gfx950"
-# Packed fp32 VALU ops are switched off for all device code.
+# Packed fp32 VALU ops are switched off for all device code.  MFMA results and
+# accumulators are kept in the VGPR form: the window kernel's lazily rescaled
+# O accumulator is otherwise mirrored between AGPRs and VGPRs every step.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-mllvm", "-amdgpu-mfma-vgpr-form=1",
              "-Wno-unused-command-line-argument"]
 
 

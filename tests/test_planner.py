@@ -133,13 +133,15 @@ def test_kernel_m_tiles_cover_largest_window(golden_plans):
         assert bgh.kernel_m_tiles(plan) * bgh.HIP_BLOCK_M >= lq.max()
 
 
-def test_launch_order_is_permutation_longest_first(golden_plans):
+def test_launch_orders_are_permutations(golden_plans):
     case = next(c for c in golden_plans if c["name"] == "c3_6x45x80")
     plan = bgh.build_plan(_spec(case))
     order = bgh.launch_order(plan).tolist()
-    assert sorted(order) == list(range(plan["n_w"]))
+    assert order == list(range(plan["n_w"]))
+    lpt = bgh.longest_first_order(plan).tolist()
+    assert sorted(lpt) == list(range(plan["n_w"]))
     cost = bgh._window_cost(plan)
-    costs = [int(cost[i]) for i in order]
+    costs = [int(cost[i]) for i in lpt]
     assert costs == sorted(costs, reverse=True)
 
 
