@@ -142,7 +142,7 @@ __device__ __forceinline__ void fill_barrier() {
 // the frame kernel are all this formula with their own grid.
 struct KeyRun {
   int n;          // keys in the run
-  int64_t base;   // token offset of frame 0 of the run
+  int base;       // token offset of frame 0 of the run
   int frame_len;  // tokens per frame of the grid the run lives on
   int t0, r0, c0; // first frame / row / column
   int rows, cols; // cuboid rows / columns per frame
@@ -150,7 +150,7 @@ struct KeyRun {
   float r_sp, r_cols;
 };
 
-__device__ __forceinline__ KeyRun make_run(int n, int64_t base, int frame_len, int t0, int r0,
+__device__ __forceinline__ KeyRun make_run(int n, int base, int frame_len, int t0, int r0,
                                            int c0, int rows, int cols, int Wg) {
   KeyRun k;
   k.n = n; k.base = base; k.frame_len = frame_len; k.t0 = t0; k.r0 = r0; k.c0 = c0;
@@ -160,14 +160,14 @@ __device__ __forceinline__ KeyRun make_run(int n, int64_t base, int frame_len, i
   return k;
 }
 
-__device__ __forceinline__ int64_t run_token(const KeyRun& k, int j) {
+// Token index of key j of the run (token counts are below 2^31, checked on entry).
+__device__ __forceinline__ int run_token(const KeyRun& k, int j) {
   const int sp = k.rows * k.cols;
   const int t = fdiv(j, sp, k.r_sp);
   const int rr = j - t * sp;
   const int row = fdiv(rr, k.cols, k.r_cols);
   const int col = rr - row * k.cols;
-  return k.base + static_cast<int64_t>(k.t0 + t) * k.frame_len +
-         static_cast<int64_t>(k.r0 + row) * k.Wg + (k.c0 + col);
+  return k.base + (k.t0 + t) * k.frame_len + (k.r0 + row) * k.Wg + (k.c0 + col);
 }
 
 template <typename T, int D>
@@ -198,9 +198,8 @@ struct Tile {
 // V transposing reads hit every bank group equally often.
 template <typename T, int D>
 __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, int seg, int wave,
-                                           int qframe, bool qvalid,
-                                           const T* __restrict__ kb, const T* __restrict__ vb,
-                                           int64_t tok, int64_t kv_tokens, float scale_log2,
+                                           int qframe, bool qvalid, __amdgpu_buffer_rsrc_t kvrsrc,
+                                           int tok_bytes, int kv_tokens, float scale_log2,
                                            T* ksh, T* vsh) {
   using TT = Tile<T, D>;
   using E = typename TT::E;
@@ -230,9 +229,8 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
     const int s = lane & 15;
     const int src_key = (s % LPK) * KPI + (lane >> 4) * (16 / LPK) + s / LPK;
     const int j = i * KN + src_key;
-    int64_t flat = run_token(run, j < run.n ? j : run.n - 1);
-    const int tokv = static_cast<int>(flat < 0 ? 0 : (flat >= kv_tokens ? kv_tokens - 1 : flat));
-    const T* base = wave == 0 ? kb : vb;
+    int tokv = run_token(run, j < run.n ? j : run.n - 1);
+    tokv = tokv < 0 ? 0 : (tokv >= kv_tokens ? kv_tokens - 1 : tokv);
     T* dst = (wave == 0 ? ksh : vsh) + (i & 1) * TILE;
     const int sub = s / LPK, pos = lane % CPK;
     static_for<NL>([&](auto qc) {
@@ -242,11 +240,12 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
         const int t1 = __builtin_amdgcn_mov_dpp(tokv, 0x150 + 8 + q, 0xf, 0xf, false);
         t = sub ? t1 : t;
       }
+      // byte offset of this lane's 16-byte chunk: lane-constant per q
       const int key = q * KPI + (lane >> 4) * (16 / LPK) + sub;
-      const int chunk = pos ^ (wave == 0 ? swz_k(key) : swz_v(key));
-      const T* src = base + static_cast<int64_t>(t) * tok + chunk * 8;
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(const_cast<T*>(src)),
-                                       (lds_void_t*)(dst + q * 512), 16, 0, 0);
+      const int chunk_off = (pos ^ (wave == 0 ? swz_k(key) : swz_v(key))) * 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          kvrsrc, (lds_void_t*)(dst + q * 512), 16,
+          static_cast<int>(__umul24(t, tok_bytes)) + chunk_off, 0, 0, 0);
     });
   };
 
@@ -259,14 +258,16 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
     const T* kbuf = ksh + (i & 1) * TILE;
     const T* vbuf = vsh + (i & 1) * TILE;
 
-    // S^T = K Q^T
+    // S^T = K Q^T: all K fragments of the step first, then the MFMA chain
+    V8 kf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kf[ks] = *reinterpret_cast<const V8*>(kbuf + (c * CPK + ((hf * KS + ks) ^ swz_k(c))) * 8);
     f32x16_t sacc = f32x16_t{};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const V8 kf =
-          *reinterpret_cast<const V8*>(kbuf + (c * CPK + ((hf * KS + ks) ^ swz_k(c))) * 8);
-      sacc = E::mma(kf, st.qf[ks], sacc);
-    }
+    for (int ks = 0; ks < KS; ++ks) sacc = E::mma(kf[ks], st.qf[ks], sacc);
+    __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);  // the K reads
+    __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);  // then the MFMAs
 
     // masking on a partial last step or inside an anchor segment
     const int nvalid = run.n - i * KN;
@@ -309,6 +310,7 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
     // O^T += V^T P^T, V^T via transposing LDS reads: the lane reads 8 bytes of
     // chunk L = 4dt + 2(g&1) + (i16&3)/2, half (i16&1), of key 16kk + 8h2 +
     // 4hf + i16/4, and receives four consecutive keys of head dim dt*32 + c.
+    V8 vt[2][DT];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
@@ -323,10 +325,13 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
               i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(const_cast<T*>(src))));
         }
         const i32x4_t vw = {half[0][0], half[0][1], half[1][0], half[1][1]};
-        const V8 vt = __builtin_bit_cast(V8, vw);
-        st.oacc[dt] = E::mma(vt, kk == 0 ? pf0 : pf1, st.oacc[dt]);
+        vt[kk][dt] = __builtin_bit_cast(V8, vw);
       }
     }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) st.oacc[dt] = E::mma(vt[kk][dt], kk == 0 ? pf0 : pf1, st.oacc[dt]);
   }
   fill_barrier();  // stages free for the next run
 }
@@ -340,7 +345,7 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
   __shared__ __attribute__((aligned(16))) T ksh[2 * KN * D];
   __shared__ __attribute__((aligned(16))) T vsh[2 * KN * D];
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int c = lane & 31, hf = lane >> 5;
   const uint32_t task = xcd_task(blockIdx.x, gridDim.x);
@@ -377,8 +382,14 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
   const int L = a.H * a.W;
   const int64_t tok = static_cast<int64_t>(a.n_heads) * D;
   const T* qb = reinterpret_cast<const T*>(a.q) + head * D;
-  const T* kb = reinterpret_cast<const T*>(a.k) + head * D;
-  const T* vb = reinterpret_cast<const T*>(a.v) + head * D;
+  // K (wavefront 0) or V (wavefront 1) of this head as a buffer resource:
+  // 32-bit byte offsets, hardware range check against the whole tensor.
+  const int tok_bytes = static_cast<int>(tok) * static_cast<int>(sizeof(T));
+  const T* kvb = reinterpret_cast<const T*>(wave == 0 ? a.k : a.v) + head * D;
+  const __amdgpu_buffer_rsrc_t kvrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(kvb), 0, static_cast<int>(a.kv_tokens) * tok_bytes - head * D * static_cast<int>(sizeof(T)),
+      0x00020000);
+  const int kv_tokens = static_cast<int>(a.kv_tokens);
   T* ob = reinterpret_cast<T*>(a.o) + head * D;
 
   // this lane's query: row m of the window, frame qframe of the window's frames
@@ -411,12 +422,12 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
     // anchor prefix (a_frames whole-chunk anchor frames), then the HR cuboid
     if (a_frames > 0 && anchor_ok) {
       KeyRun ar = make_run(a_frames * sp_a, 0, h_a * w_a, 0, kh0_a, kw0_a, kh_l_a, kw_l_a, w_a);
-      attend_run<T, D>(st, ar, -1, wave, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2,
+      attend_run<T, D>(st, ar, -1, wave, qframe, qvalid, kvrsrc, tok_bytes, kv_tokens, a.scale_log2,
                        ksh, vsh);
     }
     if (sp_hr > 0 && kv_tl > 0) {
       KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
-      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2,
+      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kvrsrc, tok_bytes, kv_tokens, a.scale_log2,
                        ksh, vsh);
     }
   } else {
@@ -426,15 +437,15 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
       const int f_lo = m0 / q_sp;
       const int f_hi = (min(lq, m0 + 64) - 1) / q_sp;
       for (int s = f_lo; s <= f_hi; ++s) {
-        KeyRun ar = make_run(sp_a, static_cast<int64_t>(s) * h_a * w_a, h_a * w_a, 0, kh0_a, kw0_a,
+        KeyRun ar = make_run(sp_a, s * h_a * w_a, h_a * w_a, 0, kh0_a, kw0_a,
                              kh_l_a, kw_l_a, w_a);
-        attend_run<T, D>(st, ar, s, wave, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2,
+        attend_run<T, D>(st, ar, s, wave, qframe, qvalid, kvrsrc, tok_bytes, kv_tokens, a.scale_log2,
                          ksh, vsh);
       }
     }
     if (sp_hr > 0 && kv_tl > 0) {
       KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
-      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kb, vb, tok, a.kv_tokens, a.scale_log2,
+      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kvrsrc, tok_bytes, kv_tokens, a.scale_log2,
                        ksh, vsh);
     }
   }
@@ -488,6 +499,10 @@ extern "C" int srdit_window_attn_fwd(const void* q, const void* k, const void* v
   SRDIT_REQUIRE(q_tokens >= 1 && kv_tokens >= 1 && q_tokens < (1LL << 31) && kv_tokens < (1LL << 31),
                 "srdit_window_attn_fwd: token counts out of range");
   SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 22), "srdit_window_attn_fwd: grid too large");
+  SRDIT_REQUIRE(kv_tokens * n_heads * head_dim * 2 < (1LL << 31) && q_tokens < (1LL << 24),
+                "srdit_window_attn_fwd: K/V must span fewer than 2^31 bytes and 2^24 tokens");
+  SRDIT_REQUIRE(static_cast<int64_t>(n_heads) * head_dim * 2 < (1LL << 24),
+                "srdit_window_attn_fwd: token stride too large");
   if (head_dim != 64 && head_dim != 128) {
     set_error("srdit_window_attn_fwd: head_dim %d unsupported (64 or 128)", head_dim);
     return SRDIT_EUNSUPPORTED;
