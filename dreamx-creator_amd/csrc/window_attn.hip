@@ -98,6 +98,7 @@ struct WinArgs {
 
 constexpr int WAVES = 2;  // wavefronts per workgroup, 32 queries each
 constexpr int KN = 32;    // keys per step
+constexpr int STAGES = 2; // LDS ring depth: the fill of step i+STAGES-1 overlaps step i
 
 // Largest growth (log2 units) of a query's running max tolerated before the
 // accumulator is rescaled.  Between rescales P = exp2(s - m_used) <= 2^TAU,
@@ -132,6 +133,27 @@ __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory")
 __device__ __forceinline__ void fill_barrier() {
   compiler_fence();
   __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  compiler_fence();
+}
+
+// As fill_barrier, but the last `keep` vector-memory operations this wavefront
+// issued may still be in flight (vmcnt(keep)); LDS reads are all retired.
+template <int N>
+__device__ __forceinline__ void waitcnt_vm_keep() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // lgkmcnt(0)
+}
+__device__ __forceinline__ void fill_barrier_keep(int keep) {
+  compiler_fence();
+  switch (keep) {  // s_waitcnt takes an immediate
+    case 0: waitcnt_vm_keep<0>(); break;
+    case 4: waitcnt_vm_keep<4>(); break;
+    case 8: waitcnt_vm_keep<8>(); break;
+    case 12: waitcnt_vm_keep<12>(); break;
+    case 16: waitcnt_vm_keep<16>(); break;
+    default: waitcnt_vm_keep<0>(); break;
+  }
   __builtin_amdgcn_s_barrier();
   compiler_fence();
 }
@@ -231,7 +253,7 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
     const int j = i * KN + src_key;
     int tokv = run_token(run, j < run.n ? j : run.n - 1);
     tokv = tokv < 0 ? 0 : (tokv >= kv_tokens ? kv_tokens - 1 : tokv);
-    T* dst = (wave == 0 ? ksh : vsh) + (i & 1) * TILE;
+    T* dst = (wave == 0 ? ksh : vsh) + (i % STAGES) * TILE;
     const int sub = s / LPK, pos = lane % CPK;
     static_for<NL>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
@@ -249,14 +271,19 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
     });
   };
 
-  fill(0);
+  // Fills run STAGES-1 steps ahead.  The wait at the top of step i leaves the
+  // fills of steps i+1 .. i+STAGES-2 in flight (one group of NL loads each).
+#pragma unroll
+  for (int f = 0; f < STAGES - 1; ++f)
+    if (f < nsteps) fill(f);
   for (int i = 0; i < nsteps; ++i) {
-    // Fill i (issued one step ago) has landed in both halves, and step i-1's
-    // LDS reads are done, so stage (i+1) & 1 may be refilled.
-    fill_barrier();
-    if (i + 1 < nsteps) fill(i + 1);
-    const T* kbuf = ksh + (i & 1) * TILE;
-    const T* vbuf = vsh + (i & 1) * TILE;
+    // Fill i has landed in both halves and step i-1's LDS reads are done, so
+    // stage (i + STAGES - 1) % STAGES (step i-1's) may be refilled.
+    const int ahead = nsteps - 1 - i < STAGES - 2 ? nsteps - 1 - i : STAGES - 2;
+    fill_barrier_keep(ahead * NL);
+    if (i + STAGES - 1 < nsteps) fill(i + STAGES - 1);
+    const T* kbuf = ksh + (i % STAGES) * TILE;
+    const T* vbuf = vsh + (i % STAGES) * TILE;
 
     // S^T = K Q^T: all K fragments of the step first, then the MFMA chain
     V8 kf[KS];
@@ -342,8 +369,8 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
   using E = typename TT::E;
   using V8 = typename TT::V8;
   constexpr int KS = TT::KS, DT = TT::DT;
-  __shared__ __attribute__((aligned(16))) T ksh[2 * KN * D];
-  __shared__ __attribute__((aligned(16))) T vsh[2 * KN * D];
+  __shared__ __attribute__((aligned(16))) T ksh[STAGES * KN * D];
+  __shared__ __attribute__((aligned(16))) T vsh[STAGES * KN * D];
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
