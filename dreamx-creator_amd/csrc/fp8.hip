@@ -1,17 +1,454 @@
-// fp8 e4m3 quantisers and scaled GEMM for gfx950 (placeholder entry points;
-// the kernels land in the next change).
+// fp8 e4m3 quantisers and the scaled fp8 GEMM for gfx950.
+//
+// Quantisers (fp8_linear.py:93-103): scale = max(amax * fl32(1/448), 1e-12),
+// q = e4m3(clamp(x / scale, +-448)) with IEEE division and round-to-nearest-even
+// conversion (v_cvt_pk_fp8_f32 writes OCP e4m3fn on gfx950).  The scale is a
+// multiply by the fp32 reciprocal because that is what `amax / 448.0` computes
+// on the GPU: torch divides a GPU tensor by a Python scalar as a multiply by
+// the scalar's fp32 reciprocal (and inductor lowers division by a constant the
+// same way); `x / scale`, with a tensor divisor, is a true division.  The row-wise
+// kernel is one wavefront per row; the per-tensor one is an amax pass
+// (integer max over the float bits of |x|, so a NaN wins as in torch's amax)
+// followed by a quantise pass that reads the amax from device memory.
+//
+// GEMM: out = bf16(a . b^T * sa * sb + bias) on v_mfma_f32_32x32x64_f8f6f4.
+// A workgroup of four wavefronts computes a 256 x 256 output tile; each
+// wavefront owns 128 x 128 (sixteen 32 x 32 accumulators).  K advances 128
+// bytes at a time through a two-stage LDS ring filled by buffer_load ... lds
+// (16 bytes per lane straight into LDS); rows past M or N read as zero through
+// the buffer descriptor's range check.  LDS rows are 128 bytes; 16-byte chunk c
+// of row r sits at chunk position c ^ ((r >> 1) & 7), which makes every
+// operand read (32 rows x 16 bytes per half-wave) conflict-free.  The MFMA's A
+// operand is the weight tile and its B operand the activation tile, so the
+// accumulator holds out^T: each lane owns one output row and runs of four
+// consecutive columns, stored as 8-byte bf16 quads.
 #include "common.h"
 
-extern "C" int srdit_fp8_quant_rowwise(const void*, int64_t, int64_t, int64_t, void*, float*, void*) {
-  srdit::set_error("srdit_fp8_quant_rowwise: not implemented yet");
-  return SRDIT_EUNSUPPORTED;
+namespace srdit {
+namespace {
+
+constexpr float kFp8Max = 448.f;
+constexpr float kInvFp8Max = 1.0f / 448.0f;   // fl32(1/448), folded at compile time
+constexpr float kScaleFloor = 1e-12f;
+
+// ---------------------------------------------------------------- quantisers
+
+// Eight consecutive elements of a row as float, plus the max of their |x|
+// bit patterns (non-negative floats order like their bits; NaN sorts last).
+template <typename T> struct Load8;
+
+template <> struct Load8<uint16_t> {  // bf16
+  static __device__ __forceinline__ void get(const void* row, int64_t c, float f[8]) {
+    const uint4 v = reinterpret_cast<const uint4*>(row)[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+
+template <> struct Load8<_Float16> {
+  static __device__ __forceinline__ void get(const void* row, int64_t c, float f[8]) {
+    const f16x8_t v = reinterpret_cast<const f16x8_t*>(row)[c];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)v[i];
+  }
+};
+
+template <> struct Load8<float> {
+  static __device__ __forceinline__ void get(const void* row, int64_t c, float f[8]) {
+    const float4 a = reinterpret_cast<const float4*>(row)[2 * c];
+    const float4 b = reinterpret_cast<const float4*>(row)[2 * c + 1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  }
+};
+
+__device__ __forceinline__ uint32_t abs_bits_max8(const float f[8], uint32_t m) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = max(m, __float_as_uint(f[i]) & 0x7fffffffu);
+  return m;
 }
-extern "C" int srdit_fp8_quant_tensor(const void*, int64_t, int64_t, int64_t, void*, float*, float*, void*) {
-  srdit::set_error("srdit_fp8_quant_tensor: not implemented yet");
-  return SRDIT_EUNSUPPORTED;
+
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
+  return v;
 }
-extern "C" int srdit_fp8_gemm(const void*, const void*, const float*, int64_t, const float*, int64_t,
-                              const void*, void*, int64_t, int64_t, int64_t, int64_t, void*) {
-  srdit::set_error("srdit_fp8_gemm: not implemented yet");
-  return SRDIT_EUNSUPPORTED;
+
+// scale = max(amax * fl32(1/448), 1e-12); a NaN amax stays NaN as torch's clamp_min keeps it.
+__device__ __forceinline__ float scale_from_amax_bits(uint32_t bits) {
+  const float s = __uint_as_float(bits) * kInvFp8Max;
+  return s < kScaleFloor ? kScaleFloor : s;
+}
+
+__device__ __forceinline__ float clamp_fp8(float q) {
+  return q > kFp8Max ? kFp8Max : (q < -kFp8Max ? -kFp8Max : q);
+}
+
+// Eight values -> eight e4m3 bytes (round to nearest even).
+__device__ __forceinline__ uint2 to_e4m3x8(const float f[8], float s) {
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = clamp_fp8(f[i] / s);
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
+  return make_uint2((uint32_t)lo, (uint32_t)hi);
+}
+
+// One wavefront per row, four rows per workgroup.  The second pass re-reads
+// the row, which is still in the L1/L2 after the first.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_rowwise_kernel(const T* __restrict__ x, int64_t M,
+                                                            int64_t K, int64_t ldx,
+                                                            uint8_t* __restrict__ xq,
+                                                            float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const T* xr = x + row * ldx;
+  const int64_t nchunk = K >> 3;
+  uint32_t amax = 0;
+  for (int64_t c = lane; c < nchunk; c += 64) {
+    float f[8];
+    Load8<T>::get(xr, c, f);
+    amax = abs_bits_max8(f, amax);
+  }
+  amax = wave_umax(amax);
+  const float s = scale_from_amax_bits(amax);
+  if (lane == 0) scale[row] = s;
+  uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
+  for (int64_t c = lane; c < nchunk; c += 64) {
+    float f[8];
+    Load8<T>::get(xr, c, f);
+    qr[c] = to_e4m3x8(f, s);
+  }
+}
+
+__global__ void clear_u32_kernel(uint32_t* p) { *p = 0u; }
+
+// Grid-stride amax: each wavefront walks rows wave_id, wave_id + n_waves, ...
+template <typename T>
+__global__ __launch_bounds__(256) void amax_kernel(const T* __restrict__ x, int64_t M, int64_t K,
+                                                   int64_t ldx, uint32_t* __restrict__ amax_ws) {
+  __shared__ uint32_t part[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t nchunk = K >> 3;
+  uint32_t amax = 0;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
+    const T* xr = x + row * ldx;
+    for (int64_t c = lane; c < nchunk; c += 64) {
+      float f[8];
+      Load8<T>::get(xr, c, f);
+      amax = abs_bits_max8(f, amax);
+    }
+  }
+  amax = wave_umax(amax);
+  if (lane == 0) part[wave] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t m = max(max(part[0], part[1]), max(part[2], part[3]));
+    atomicMax(amax_ws, m);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void quant_tensor_kernel(const T* __restrict__ x, int64_t M,
+                                                           int64_t K, int64_t ldx,
+                                                           uint8_t* __restrict__ xq,
+                                                           float* __restrict__ scale,
+                                                           const uint32_t* __restrict__ amax_ws) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float s = scale_from_amax_bits(*amax_ws);
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
+  const int64_t nchunk = K >> 3;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
+    const T* xr = x + row * ldx;
+    uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
+    for (int64_t c = lane; c < nchunk; c += 64) {
+      float f[8];
+      Load8<T>::get(xr, c, f);
+      qr[c] = to_e4m3x8(f, s);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------- GEMM
+
+constexpr int GT = 256;                       // tile rows (M) and columns (N)
+constexpr int GK = 128;                       // K bytes per stage
+constexpr int G_OPERAND_BYTES = GT * GK;      // 32 KB per operand per stage
+constexpr int G_STAGE_BYTES = 2 * G_OPERAND_BYTES;
+constexpr int G_GROUP_M = 8;                  // M tiles per raster group
+
+struct GemmArgs {
+  const uint8_t* a;      // [M, K]
+  const uint8_t* b;      // [N, K]
+  const float* sa;       // [1] or [M]
+  const float* sb;       // [1] or [N]
+  const uint16_t* bias;  // [N] bf16 or null
+  uint16_t* out;         // [M, ldo] bf16
+  int M, N, K;
+  int64_t ldo;
+  int sa_per_row, sb_per_col;
+  int tiles_m, tiles_n;
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ i32x8_t read_frag(const uint8_t* lds, int off_lo, int off_hi) {
+  const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(lds + off_lo);
+  const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(lds + off_hi);
+  return i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+__global__ __launch_bounds__(256) void fp8_gemm_kernel(const GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G_STAGE_BYTES];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+
+  // Tile raster: XCD-contiguous task ranges, then groups of G_GROUP_M tile rows
+  // walked column by column so the workgroups sharing an L2 share A and B tiles.
+  const uint32_t n_tasks = (uint32_t)g.tiles_m * g.tiles_n;
+  const uint32_t task = xcd_task(blockIdx.x, n_tasks);
+  const int width = G_GROUP_M * g.tiles_n;
+  const int group = task / width;
+  const int first_m = group * G_GROUP_M;
+  const int gsize = min(g.tiles_m - first_m, G_GROUP_M);
+  const int tm = first_m + (int)(task % width) % gsize;
+  const int tn = (int)(task % width) / gsize;
+  const int m0 = tm * GT, n0 = tn * GT;
+
+  // Buffer descriptors over this tile's rows to the end of each operand:
+  // reads of rows >= M (or N) fall outside num_records and return zero.
+  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.a + (int64_t)m0 * g.K), 0, (g.M - m0) * g.K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.b + (int64_t)n0 * g.K), 0, (g.N - n0) * g.K, 0x00020000);
+
+  // Fill mapping: instruction q = wave*8 + j writes LDS bytes [q*1024, +1024),
+  // lane l -> tile row q*8 + l/8, chunk position l%8, which holds source chunk
+  // (l%8) ^ ((row >> 1) & 7) = (l%8) ^ ((4*(j&1) + (l>>4)) & 7).
+  const int frow = wave * 64 + (lane >> 3);
+  const int fpos = lane & 7;
+  const int fchunk0 = fpos ^ ((lane >> 4) & 7);
+  const int fchunk1 = fpos ^ ((4 + (lane >> 4)) & 7);
+  const int fvoff0 = frow * g.K + fchunk0 * 16;
+  const int fvoff1 = frow * g.K + fchunk1 * 16;
+
+  auto fill = [&](int stage, int kt) {
+    uint8_t* base = smem + stage * G_STAGE_BYTES + wave * 8192;
+    const int koff = kt * GK;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int voff = ((j & 1) ? fvoff1 : fvoff0) + j * 8 * g.K;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (lds_void_t*)(base + j * 1024), 16, voff,
+                                               koff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs_b, (lds_void_t*)(base + G_OPERAND_BYTES + j * 1024), 16, voff, koff, 0, 0);
+    }
+  };
+
+  // Operand read offsets: row (l & 31) of a 32-row subtile, chunks
+  // kk*4 + (l>>5)*2 + h at position chunk ^ ((l & 31) >> 1 & 7).
+  const int rrow = lane & 31;
+  const int rswz = (rrow >> 1) & 7;
+  int roff[2][2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      roff[kk][h] = rrow * GK + (((kk * 4 + (lane >> 5) * 2 + h) ^ rswz) * 16);
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = g.K / GK;
+  fill(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    if (kt + 1 < nk) fill((kt + 1) & 1, kt + 1);
+    const uint8_t* sa_ = smem + (kt & 1) * G_STAGE_BYTES;               // activation tile
+    const uint8_t* sb_ = sa_ + G_OPERAND_BYTES;                          // weight tile
+    const uint8_t* ta = sa_ + wm * 128 * GK;
+    const uint8_t* tb = sb_ + wn * 128 * GK;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      i32x8_t fw[4], fx[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fw[i] = read_frag(tb + i * 32 * GK, roff[kk][0], roff[kk][1]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fx[j] = read_frag(ta + j * 32 * GK, roff[kk][0], roff[kk][1]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[i], fx[j], acc[i][j], 0, 0,
+                                                                      0, 0, 0, 0);
+    }
+  }
+
+  // Epilogue: acc[i][j] is the 32 x 32 block out^T[n-subtile i][m-subtile j];
+  // lane l holds row m = .. + (l & 31) and columns n = .. + 8*(r/4) + 4*(l/32) + r%4.
+  const int mrow = lane & 31;
+  const int ncol = 4 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = m0 + wm * 128 + j * 32 + mrow;
+    if (m >= g.M) continue;
+    const float sa = g.sa[g.sa_per_row ? m : 0];
+    uint16_t* orow = g.out + (int64_t)m * g.ldo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * 128 + i * 32 + 8 * q + ncol;
+        if (n >= g.N) continue;
+        float sb[4], bias[4];
+        if (g.sb_per_col) {
+          const float4 v = *reinterpret_cast<const float4*>(g.sb + n);
+          sb[0] = v.x; sb[1] = v.y; sb[2] = v.z; sb[3] = v.w;
+        } else {
+          sb[0] = sb[1] = sb[2] = sb[3] = g.sb[0];
+        }
+        if (g.bias) {
+          const uint2 bv = *reinterpret_cast<const uint2*>(g.bias + n);
+          bias[0] = __uint_as_float(bv.x << 16);
+          bias[1] = __uint_as_float(bv.x & 0xffff0000u);
+          bias[2] = __uint_as_float(bv.y << 16);
+          bias[3] = __uint_as_float(bv.y & 0xffff0000u);
+        } else {
+          bias[0] = bias[1] = bias[2] = bias[3] = 0.f;
+        }
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * q + r] * sa * sb[r] + bias[r];
+        typedef float f32x2v __attribute__((ext_vector_type(2)));
+        typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+        const bf16x2v p0 = __builtin_convertvector(f32x2v{v[0], v[1]}, bf16x2v);
+        const bf16x2v p1 = __builtin_convertvector(f32x2v{v[2], v[3]}, bf16x2v);
+        uint2 packed;
+        packed.x = __builtin_bit_cast(uint32_t, p0);
+        packed.y = __builtin_bit_cast(uint32_t, p1);
+        *reinterpret_cast<uint2*>(orow + n) = packed;
+      }
+    }
+  }
+}
+
+template <typename Launch>
+int dispatch_quant_dtype(int dtype, Launch&& launch) {
+  switch (dtype) {
+    case SRDIT_DTYPE_BF16: return launch((const uint16_t*)nullptr);
+    case SRDIT_DTYPE_FP16: return launch((const _Float16*)nullptr);
+    case SRDIT_DTYPE_FP32: return launch((const float*)nullptr);
+    default:
+      set_error("fp8 quantiser: dtype %d is not bf16 (0), fp16 (1) or fp32 (2)", dtype);
+      return SRDIT_EUNSUPPORTED;
+  }
+}
+
+int check_quant_args(const char* who, const void* x, int64_t M, int64_t K, int64_t ldx,
+                     const void* xq, const float* scale) {
+  SRDIT_REQUIRE(x && xq && scale, "%s: null pointer", who);
+  SRDIT_REQUIRE(M > 0 && K > 0, "%s: M=%lld K=%lld must be positive", who, (long long)M,
+                (long long)K);
+  SRDIT_REQUIRE(K % 8 == 0 && ldx % 8 == 0 && ldx >= K,
+                "%s: K=%lld and ldx=%lld must be multiples of 8 with ldx >= K", who,
+                (long long)K, (long long)ldx);
+  SRDIT_REQUIRE(aligned16(x) && aligned16(xq), "%s: x and xq must be 16-byte aligned", who);
+  return SRDIT_OK;
+}
+
+}  // namespace
+}  // namespace srdit
+
+using namespace srdit;
+
+extern "C" int srdit_fp8_quant_rowwise(const void* x, int64_t M, int64_t K, int64_t ldx,
+                                       int dtype, void* xq, float* scale, void* stream) {
+  if (int rc = check_quant_args("srdit_fp8_quant_rowwise", x, M, K, ldx, xq, scale)) return rc;
+  SRDIT_REQUIRE(M < (int64_t(1) << 33), "srdit_fp8_quant_rowwise: M=%lld too large", (long long)M);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dispatch_quant_dtype(dtype, [&](auto tag) -> int {
+    using T = std::remove_const_t<std::remove_pointer_t<decltype(tag)>>;
+    const unsigned blocks = (unsigned)((M + 3) / 4);
+    quant_rowwise_kernel<T><<<blocks, 256, 0, s>>>(static_cast<const T*>(x), M, K, ldx,
+                                                   static_cast<uint8_t*>(xq), scale);
+    SRDIT_LAUNCH_CHECK("quant_rowwise_kernel");
+    return SRDIT_OK;
+  });
+}
+
+extern "C" int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype,
+                                      void* xq, float* scale, uint32_t* amax_ws, void* stream) {
+  if (int rc = check_quant_args("srdit_fp8_quant_tensor", x, M, K, ldx, xq, scale)) return rc;
+  SRDIT_REQUIRE(amax_ws, "srdit_fp8_quant_tensor: null amax workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dispatch_quant_dtype(dtype, [&](auto tag) -> int {
+    using T = std::remove_const_t<std::remove_pointer_t<decltype(tag)>>;
+    const int64_t rows4 = (M + 3) / 4;
+    const unsigned blocks = (unsigned)(rows4 < 4096 ? rows4 : 4096);
+    clear_u32_kernel<<<1, 1, 0, s>>>(amax_ws);
+    SRDIT_LAUNCH_CHECK("clear_u32_kernel");
+    amax_kernel<T><<<blocks, 256, 0, s>>>(static_cast<const T*>(x), M, K, ldx, amax_ws);
+    SRDIT_LAUNCH_CHECK("amax_kernel");
+    quant_tensor_kernel<T><<<blocks, 256, 0, s>>>(static_cast<const T*>(x), M, K, ldx,
+                                                  static_cast<uint8_t*>(xq), scale, amax_ws);
+    SRDIT_LAUNCH_CHECK("quant_tensor_kernel");
+    return SRDIT_OK;
+  });
+}
+
+extern "C" int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_rows,
+                              const float* sb, int64_t sb_cols, const void* bias, void* out,
+                              int64_t M, int64_t N, int64_t K, int64_t ldo, void* stream) {
+  SRDIT_REQUIRE(a && b && sa && sb && out, "srdit_fp8_gemm: null pointer");
+  SRDIT_REQUIRE(M > 0 && N > 0 && K > 0, "srdit_fp8_gemm: M, N, K must be positive");
+  SRDIT_REQUIRE(K % 128 == 0, "srdit_fp8_gemm: K=%lld must be a multiple of 128", (long long)K);
+  SRDIT_REQUIRE(N % 16 == 0, "srdit_fp8_gemm: N=%lld must be a multiple of 16", (long long)N);
+  SRDIT_REQUIRE(ldo >= N && ldo % 4 == 0, "srdit_fp8_gemm: ldo=%lld must be >= N and a multiple of 4",
+                (long long)ldo);
+  SRDIT_REQUIRE(M * K < (int64_t(1) << 31) && N * K < (int64_t(1) << 31),
+                "srdit_fp8_gemm: M*K and N*K must be below 2^31 (M=%lld N=%lld K=%lld)",
+                (long long)M, (long long)N, (long long)K);
+  SRDIT_REQUIRE(sa_rows == 1 || sa_rows == M, "srdit_fp8_gemm: sa_rows=%lld must be 1 or M",
+                (long long)sa_rows);
+  SRDIT_REQUIRE(sb_cols == 1 || sb_cols == N, "srdit_fp8_gemm: sb_cols=%lld must be 1 or N",
+                (long long)sb_cols);
+  SRDIT_REQUIRE(aligned16(a) && aligned16(b) && aligned16(sb) && aligned16(out) &&
+                    (!bias || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0),
+                "srdit_fp8_gemm: a, b, sb, out must be 16-byte aligned and bias 8-byte aligned");
+  GemmArgs g;
+  g.a = static_cast<const uint8_t*>(a);
+  g.b = static_cast<const uint8_t*>(b);
+  g.sa = sa;
+  g.sb = sb;
+  g.bias = static_cast<const uint16_t*>(bias);
+  g.out = static_cast<uint16_t*>(out);
+  g.M = (int)M;
+  g.N = (int)N;
+  g.K = (int)K;
+  g.ldo = ldo;
+  g.sa_per_row = sa_rows == M && M > 1;
+  g.sb_per_col = sb_cols == N && N > 1;
+  g.tiles_m = (int)((M + GT - 1) / GT);
+  g.tiles_n = (int)((N + GT - 1) / GT);
+  const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
+  SRDIT_REQUIRE(tiles < (int64_t(1) << 31), "srdit_fp8_gemm: too many tiles");
+  fp8_gemm_kernel<<<(unsigned)tiles, 256, 0, static_cast<hipStream_t>(stream)>>>(g);
+  SRDIT_LAUNCH_CHECK("fp8_gemm_kernel");
+  return SRDIT_OK;
 }

@@ -25,8 +25,9 @@ SIGNATURES = {
                                        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                        _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_int,
                                        _c_int, _c_p]),
-    "srdit_fp8_quant_rowwise": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
-    "srdit_fp8_quant_tensor": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p]),
+    "srdit_fp8_quant_rowwise": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p]),
+    "srdit_fp8_quant_tensor": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
+                                        _c_p]),
     "srdit_fp8_gemm": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p,
                                 _c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
     "srdit_last_error": (_c_int, [ctypes.c_char_p, _c_int]),
@@ -85,23 +86,60 @@ def window_attn_fwd(q, k, v, o, params, order, *, n_w, m_tiles, p_stride, hr_bas
     _check(rc, "srdit_window_attn_fwd")
 
 
-def fp8_quant_rowwise(x, xq, scale):
+QUANT_DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def _quant_args(x, xq):
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError(f"fp8 quantiser needs a 2-D input with unit column stride, got "
+                         f"shape {tuple(x.shape)} strides {x.stride()}")
+    if x.dtype not in QUANT_DTYPE_CODES:
+        raise ValueError(f"fp8 quantiser input must be bf16, fp16 or fp32, got {x.dtype}")
+    if xq.dtype != torch.float8_e4m3fn or tuple(xq.shape) != tuple(x.shape) or not xq.is_contiguous():
+        raise ValueError("fp8 quantiser output must be a contiguous float8_e4m3fn tensor "
+                         "shaped like the input")
     M, K = x.shape
-    rc = load().srdit_fp8_quant_rowwise(_ptr(x), M, K, x.stride(0), _ptr(xq), _ptr(scale),
+    return M, K, x.stride(0), QUANT_DTYPE_CODES[x.dtype]
+
+
+def fp8_quant_rowwise(x, xq, scale):
+    M, K, ldx, dt = _quant_args(x, xq)
+    if scale.dtype != torch.float32 or scale.numel() != M:
+        raise ValueError(f"row-wise scale must be {M} float32 values")
+    rc = load().srdit_fp8_quant_rowwise(_ptr(x), M, K, ldx, dt, _ptr(xq), _ptr(scale),
                                         _stream(x.device))
     _check(rc, "srdit_fp8_quant_rowwise")
 
 
 def fp8_quant_tensor(x, xq, scale, amax_ws):
-    M, K = x.shape
-    rc = load().srdit_fp8_quant_tensor(_ptr(x), M, K, x.stride(0), _ptr(xq), _ptr(scale),
+    M, K, ldx, dt = _quant_args(x, xq)
+    if scale.dtype != torch.float32 or scale.numel() != 1:
+        raise ValueError("per-tensor scale must be one float32 value")
+    if amax_ws.numel() * amax_ws.element_size() < 4:
+        raise ValueError("amax workspace must hold at least 4 bytes")
+    rc = load().srdit_fp8_quant_tensor(_ptr(x), M, K, ldx, dt, _ptr(xq), _ptr(scale),
                                        _ptr(amax_ws), _stream(x.device))
     _check(rc, "srdit_fp8_quant_tensor")
 
 
 def fp8_gemm(a, b, sa, sb, bias, out):
+    """out[M, N] (bf16, unit column stride) = a[M, K] . b[N, K]^T * sa * sb + bias."""
+    for name, t in (("a", a), ("b", b)):
+        if t.dtype != torch.float8_e4m3fn or t.dim() != 2 or not t.is_contiguous():
+            raise ValueError(f"fp8_gemm: {name} must be a contiguous 2-D float8_e4m3fn tensor")
     M, K = a.shape
     N = b.shape[0]
+    if b.shape[1] != K:
+        raise ValueError(f"fp8_gemm: inner dims differ ({K} vs {b.shape[1]})")
+    for name, t in (("sa", sa), ("sb", sb)):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"fp8_gemm: {name} must be contiguous float32")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.numel() != N
+                             or not bias.is_contiguous()):
+        raise ValueError(f"fp8_gemm: bias must be {N} contiguous bf16 values")
+    if out.dtype != torch.bfloat16 or out.dim() != 2 or tuple(out.shape) != (M, N) \
+            or out.stride(1) != 1:
+        raise ValueError(f"fp8_gemm: out must be bf16 [{M}, {N}] with unit column stride")
     rc = load().srdit_fp8_gemm(_ptr(a), _ptr(b), _ptr(sa), int(sa.numel()), _ptr(sb),
                                int(sb.numel()), _ptr(bias), _ptr(out), M, N, K,
                                out.stride(0), _stream(a.device))

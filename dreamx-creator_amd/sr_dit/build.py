@@ -20,13 +20,15 @@ INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(PKG_DIR, "libsrdit_hip.so")
 
 ARCH = "gfx950"
-# Packed fp32 VALU ops are switched off for all device code.  MFMA results and
-# accumulators are kept in the VGPR form: the window kernel's lazily rescaled
-# O accumulator is otherwise mirrored between AGPRs and VGPRs every step.
-HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
+# Packed fp32 VALU ops are switched off for all device code.
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-             "-mllvm", "-amdgpu-mfma-vgpr-form=1",
              "-Wno-unused-command-line-argument"]
+# Per-source additions.  The window kernel keeps its MFMA results and
+# accumulators in the VGPR form: its lazily rescaled O accumulator is otherwise
+# mirrored between AGPRs and VGPRs every step.  The GEMM needs the AGPRs for its
+# 256 accumulator registers per lane, so it keeps the default.
+FILE_FLAGS = {"window_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc() -> str:
@@ -40,22 +42,44 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
+def _run(cmds, verbose):
+    """Run compiler commands in parallel; raise with the filtered stderr on failure."""
+    noise = "is not a recognized feature for this target"
+    procs = []
+    for cmd in cmds:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                            text=True)))
+    errors = []
+    for cmd, p in procs:
+        _, err = p.communicate()
+        err = "\n".join(l for l in err.splitlines() if noise not in l)
+        if p.returncode != 0:
+            errors.append(f"{os.path.basename(cmd[-3])}: hipcc failed ({p.returncode}):\n{err}")
+        elif verbose and err.strip():
+            print(err, file=sys.stderr)
+    if errors:
+        raise RuntimeError("\n".join(errors))
+
+
 def build(verbose: bool = False) -> str:
     """Compile the library; returns its path.  Always recompiles."""
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
+    objdir = os.path.join(PKG_DIR, "_obj")
+    os.makedirs(objdir, exist_ok=True)
+    cc = hipcc()
+    objs, cmds = [], []
+    for src in srcs:
+        obj = os.path.join(objdir, os.path.basename(src) + ".o")
+        objs.append(obj)
+        cmds.append([cc, *HIP_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []),
+                     f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
+    _run(cmds, verbose)
     tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
+    _run([[cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]], verbose)
     os.replace(tmp, OUT)
     return OUT
 

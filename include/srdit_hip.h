@@ -26,6 +26,7 @@ extern "C" {
 /* element type codes */
 #define SRDIT_DTYPE_BF16 0
 #define SRDIT_DTYPE_FP16 1
+#define SRDIT_DTYPE_FP32 2  /* fp8 quantiser input only */
 
 /*
  * Block-grid window attention, forward.
@@ -57,25 +58,30 @@ int srdit_window_attn_fwd(const void* q, const void* k, const void* v, void* o,
                           int dtype, void* stream);
 
 /*
- * Row-wise fp8 e4m3 quantiser: for each row of x [M, K] (bf16),
- *   scale[m] = max(amax(|x[m,:]|) / 448, 1e-12);  xq = e4m3(clamp(x / scale, +-448))
- * with round-to-nearest-even.  Replaces _quantize_rowwise_impl
- * (video_refiner/wan/modules/sr_dit/fp8_linear.py:93-103).
- * xq [M, K] uint8 (OCP e4m3fn bytes), scale [M] float.
+ * Row-wise fp8 e4m3 quantiser: for each row of x [M, K] (row stride ldx),
+ *   scale[m] = max(amax(|x[m,:]|) * fl32(1/448), 1e-12)   (fp32; what torch computes
+ *              for amax / 448.0 on a GPU tensor)
+ *   xq[m,k]  = e4m3(clamp(x[m,k] / scale[m], -448, 448))   (round to nearest even)
+ * Replaces _quantize_rowwise_impl (video_refiner/wan/modules/sr_dit/fp8_linear.py:93-103),
+ * used for the activation on every Fp8Linear call and for the weight once.
+ * x is bf16, fp16 or fp32 (dtype); xq [M, K] contiguous OCP e4m3fn bytes;
+ * scale [M] float.  K % 8 == 0, ldx % 8 == 0.
  */
-int srdit_fp8_quant_rowwise(const void* x, int64_t M, int64_t K, int64_t ldx,
+int srdit_fp8_quant_rowwise(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype,
                             void* xq, float* scale, void* stream);
 
 /*
- * Per-tensor fp8 e4m3 quantiser, two launches on `stream`:
- * amax over all of x [M, K] (bf16) into amax_ws (one float, device; cleared by
- * the call), then scale[0] = max(amax / 448, 1e-12) and xq = e4m3(x / scale).
- * The per-tensor mode of the fp8 Linear; the reference quantises row-wise only
- * (fp8_linear.py:93-103) and names per-tensor as its faster alternative
- * (fp8_linear.py:22, :31-38).
+ * Per-tensor fp8 e4m3 quantiser, three launches on `stream`: clear amax_ws (a
+ * fill kernel, so the sequence can be captured in a graph), amax of |x| over
+ * all of x [M, K] into amax_ws (one uint32 holding the float's bits, device),
+ * then scale[0] = max(amax * fl32(1/448), 1e-12) and xq = e4m3(clamp(x / scale, +-448)).
+ * The per-tensor mode of the fp8 Linear: the reference quantises row-wise
+ * (fp8_linear.py:93-103) and names per-tensor scaling as its faster
+ * alternative (fp8_linear.py:22, :31-38).  Same dtype and layout rules as the
+ * row-wise quantiser.
  */
-int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64_t ldx,
-                           void* xq, float* scale, float* amax_ws, void* stream);
+int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype,
+                           void* xq, float* scale, uint32_t* amax_ws, void* stream);
 
 /*
  * Scaled fp8 GEMM:  out[m, n] = bf16( sum_k a[m,k] b[n,k] * sa[m or 0] * sb[n or 0]
@@ -84,8 +90,10 @@ int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64_t ldx,
  * layout), fp32 accumulate, bias bf16 [N] or NULL, out bf16 [M, N] with row
  * stride ldo.  sa_rows is 1 (per-tensor) or M (row-wise); sb_cols is 1 or N.
  * Replaces torch._scaled_mm(xq, w_fp8.t(), scale_a, scale_b, bias,
- * out_dtype=bf16) in Fp8Linear.forward (fp8_linear.py:282-297).
- * Requires K % 128 == 0.
+ * out_dtype=bf16) in Fp8Linear.forward (fp8_linear.py:282-297); the bias is
+ * applied to the fp32 value before the single bf16 rounding, as the reference's
+ * epilogue does (fp8_linear.py:238-241).
+ * Requires K % 128 == 0, N % 16 == 0, ldo % 4 == 0, M*K and N*K below 2^31.
  */
 int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_rows,
                    const float* sb, int64_t sb_cols, const void* bias, void* out,

@@ -1,0 +1,264 @@
+"""fp8 quantisers and scaled GEMM on the GPU, through the C ABI, against the oracle.
+
+Quantisers: bit-exact (codes and scales) against the numpy oracle and against
+the reference's formula (fp8_linear.py:96-103) evaluated with torch on the GPU.
+GEMM: against the float64 dequantised product, per element within the bf16
+rounding of the result plus an fp32-accumulation allowance of 2^-12 times the
+sum of |terms| of that element.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as of
+
+pytestmark = pytest.mark.gpu
+
+F8 = torch.float8_e4m3fn
+
+
+def _lib():
+    from sr_dit import _lib
+    return _lib
+
+
+def _rand(shape, dtype, seed, spread=6.0):
+    g = torch.Generator("cpu").manual_seed(seed)
+    rows = torch.empty(shape[0], 1).uniform_(-spread, spread, generator=g).exp()
+    return (torch.randn(shape, generator=g) * rows).to(dtype)
+
+
+def _torch_rowwise(x):
+    """fp8_linear.py:96-103 with torch ops (on whatever device x is)."""
+    amax = x.abs().amax(dim=-1, keepdim=True).float()
+    scale = (amax / 448.0).clamp_min(1e-12)
+    q = (x.float() / scale).clamp(-448.0, 448.0).to(F8)
+    return q, scale
+
+
+QUANT_CASES = [((1, 8), torch.bfloat16), ((3, 136), torch.bfloat16), ((257, 3072), torch.bfloat16),
+               ((64, 14336), torch.bfloat16), ((5, 64), torch.float16), ((9, 200), torch.float32),
+               ((130, 1024), torch.float32)]
+
+
+@pytest.mark.parametrize("shape,dtype", QUANT_CASES, ids=lambda v: str(v))
+def test_quant_rowwise_bit_exact(shape, dtype):
+    print(f"quant_rowwise {shape} {dtype}", flush=True)
+    x = _rand(shape, dtype, seed=shape[0] * 7 + shape[1])
+    if shape[0] > 2:
+        x[1] = 0
+    q_ref, s_ref = of.quantize_rowwise(x.float().numpy())
+    xd = x.cuda()
+    q = torch.empty(shape, dtype=F8, device="cuda")
+    s = torch.empty(shape[0], dtype=torch.float32, device="cuda")
+    _lib().fp8_quant_rowwise(xd, q, s)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    qt, st = _torch_rowwise(xd)
+    assert torch.equal(q.view(torch.uint8), qt.view(torch.uint8))
+    assert torch.equal(s, st.reshape(-1))
+
+
+def test_quant_rowwise_strided_rows():
+    big = _rand((40, 512), torch.bfloat16, seed=11).cuda()
+    x = big[:, 128:128 + 256]                       # ldx 512, K 256, 256-byte offset
+    q = torch.empty((40, 256), dtype=F8, device="cuda")
+    s = torch.empty(40, dtype=torch.float32, device="cuda")
+    _lib().fp8_quant_rowwise(x, q, s)
+    q_ref, s_ref = of.quantize_rowwise(x.float().cpu().numpy())
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+
+
+@pytest.mark.parametrize("shape,dtype", [((1, 8), torch.bfloat16), ((257, 3072), torch.bfloat16),
+                                         ((4096, 1024), torch.bfloat16), ((9, 200), torch.float32)],
+                         ids=lambda v: str(v))
+def test_quant_tensor_bit_exact(shape, dtype):
+    print(f"quant_tensor {shape} {dtype}", flush=True)
+    x = _rand(shape, dtype, seed=shape[0] + 3)
+    q_ref, s_ref = of.quantize_tensor(x.float().numpy())
+    xd = x.cuda()
+    q = torch.empty(shape, dtype=F8, device="cuda")
+    s = torch.empty(1, dtype=torch.float32, device="cuda")
+    ws = torch.full((1,), 12345, dtype=torch.int32, device="cuda")   # stale contents are cleared
+    _lib().fp8_quant_tensor(xd, q, s, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_quant_rejects_bad_shapes():
+    x = torch.zeros((4, 12), dtype=torch.bfloat16, device="cuda")     # K % 8 != 0
+    q = torch.empty((4, 12), dtype=F8, device="cuda")
+    s = torch.empty(4, dtype=torch.float32, device="cuda")
+    with pytest.raises(RuntimeError, match="multiples of 8"):
+        _lib().fp8_quant_rowwise(x, q, s)
+
+
+def _quant_codes(shape, seed, spread=2.0):
+    x = _rand(shape, torch.float32, seed, spread).numpy()
+    return of.quantize_rowwise(x)
+
+
+def _gemm_check(out, a_codes, b_codes, sa, sb, bias):
+    ref = of.gemm_dequant(a_codes, b_codes, sa, sb, bias)
+    t = of.e4m3_decode_table()
+    sa_, sb_ = np.asarray(sa, np.float64).reshape(-1), np.asarray(sb, np.float64).reshape(-1)
+    absum = np.abs(t[a_codes]) @ np.abs(t[b_codes]).T
+    absum *= np.abs(sa_[:, None] if sa_.size > 1 else sa_[0])
+    absum *= np.abs(sb_[None, :] if sb_.size > 1 else sb_[0])
+    got = out.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref)
+    tol = 2.0 ** -8 * np.abs(ref) + 2.0 ** -12 * absum + 1e-30
+    worst = np.max(err / tol)
+    assert worst <= 1.0, f"worst err/tol {worst:.3f}, max err {err.max():.3e}"
+
+
+GEMM_CASES = [
+    # M, N, K, row-wise a scale, per-column b scale, bias
+    (256, 256, 128, True, True, True),
+    (300, 272, 384, True, True, True),       # ragged M and N tiles
+    (64, 32, 256, False, False, False),      # per-tensor scales
+    (513, 1040, 1152, True, False, True),
+    (1, 16, 128, True, True, True),
+    (1000, 3072, 3072, True, True, True),
+]
+
+
+@pytest.mark.parametrize("M,N,K,rs,cs,use_bias", GEMM_CASES, ids=lambda v: str(v))
+def test_gemm_matches_dequantised_product(M, N, K, rs, cs, use_bias):
+    print(f"gemm M={M} N={N} K={K} rows={rs} cols={cs} bias={use_bias}", flush=True)
+    a, sa = _quant_codes((M, K), seed=M + K)
+    b, sb = _quant_codes((N, K), seed=N * 3 + K)
+    if not rs:
+        sa = np.float32([0.75])
+    if not cs:
+        sb = np.float32([1.25])
+    g = torch.Generator("cpu").manual_seed(5)
+    bias = (torch.randn(N, generator=g) * 4).to(torch.bfloat16) if use_bias else None
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _lib().fp8_gemm(torch.from_numpy(a).view(F8).cuda(), torch.from_numpy(b).view(F8).cuda(),
+                    torch.from_numpy(sa).cuda(), torch.from_numpy(sb).cuda(),
+                    bias.cuda() if bias is not None else None, out)
+    torch.cuda.synchronize()
+    _gemm_check(out, a, b, sa, sb, bias.float().numpy() if bias is not None else None)
+
+
+def test_gemm_strided_output_leaves_padding():
+    M, N, K, ldo = 96, 48, 256, 64
+    a, sa = _quant_codes((M, K), seed=1)
+    b, sb = _quant_codes((N, K), seed=2)
+    buf = torch.full((M, ldo), 7.0, dtype=torch.bfloat16, device="cuda")
+    out = buf[:, :N]
+    _lib().fp8_gemm(torch.from_numpy(a).view(F8).cuda(), torch.from_numpy(b).view(F8).cuda(),
+                    torch.from_numpy(sa).cuda(), torch.from_numpy(sb).cuda(), None, out)
+    torch.cuda.synchronize()
+    _gemm_check(out, a, b, sa, sb, None)
+    assert torch.all(buf[:, N:] == 7.0)
+
+
+@pytest.mark.parametrize("M,N,K", [(21600, 3072, 3072), (2048, 14336, 3072), (2048, 3072, 14336)])
+def test_gemm_full_size_against_fp32_matmul(M, N, K):
+    """Production shapes (q/k/v/o, ffn.0, ffn.2) against torch's fp32 matmul of the
+    dequantised operands, with the same per-element bound."""
+    print(f"gemm full-size M={M} N={N} K={K}", flush=True)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    x = _rand((M, K), torch.bfloat16, seed=21, spread=1.0).cuda()
+    w = (_rand((N, K), torch.float32, seed=22, spread=0.5) * 0.02).to(torch.bfloat16).cuda()
+    xq, xs = _torch_rowwise(x)
+    wq, ws = _torch_rowwise(w)
+    bias = (torch.randn(N, generator=torch.Generator("cpu").manual_seed(3)) * 0.1).to(torch.bfloat16).cuda()
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    _lib().fp8_gemm(xq.contiguous(), wq.contiguous(), xs.reshape(-1).contiguous(),
+                    ws.reshape(-1).contiguous(), bias, out)
+    A, B = xq.float(), wq.float()
+    ref = (A @ B.T) * xs * ws.reshape(1, -1) + bias.float()
+    absum = (A.abs() @ B.abs().T) * xs * ws.reshape(1, -1)
+    tol = 2.0 ** -8 * ref.abs() + 2.0 ** -12 * absum + 2.0 ** -20 * absum.max()
+    worst = ((out.float() - ref).abs() / tol).max().item()
+    assert worst <= 1.0, worst
+
+
+def test_fp8_linear_rowwise_and_tensor():
+    from sr_dit.fp8_linear import Fp8Linear
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(384, 272).to(torch.bfloat16).cuda()
+    x = torch.randn(2, 150, 384, dtype=torch.bfloat16, device="cuda")
+    for scaling in ("rowwise", "tensor"):
+        m = Fp8Linear.from_linear(lin, scaling=scaling)
+        y = m(x)
+        assert y.shape == (2, 150, 272) and y.dtype == torch.bfloat16
+        # reference semantics with torch ops: quantise, dequantised fp32 product, bias
+        x2 = x.reshape(-1, 384)
+        if scaling == "rowwise":
+            xq, xs = _torch_rowwise(x2)
+            wq, ws = _torch_rowwise(lin.weight.detach())
+            ws = ws.reshape(1, -1)
+        else:
+            def tq(t):
+                s = (t.abs().amax().float() / 448.0).clamp_min(1e-12)
+                return (t.float() / s).clamp(-448, 448).to(F8), s
+            xq, xs = tq(x2)
+            wq, ws = tq(lin.weight.detach())
+        assert torch.equal(m.weight_fp8.view(torch.uint8), wq.view(torch.uint8))
+        ref = (xq.float() @ wq.float().T) * xs * ws + lin.bias.float()
+        err = (y.reshape(-1, 272).float() - ref).abs()
+        assert err.max().item() <= 2.0 ** -7 * ref.abs().max().item(), scaling
+        # .to(bf16) keeps the fp8 buffers' dtypes (fp8_linear.py:260-280)
+        m2 = m.to(torch.bfloat16)
+        assert m2.weight_fp8.dtype == F8 and m2.weight_scale.dtype == torch.float32
+        assert m2.weight.numel() == 0 and m2.weight.dtype == torch.bfloat16
+
+
+def test_convert_linears_to_fp8_swaps_blocks_in_range():
+    from sr_dit.fp8_linear import Fp8Linear, TARGETS_ALL, convert_linears_to_fp8
+
+    class Attn(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            for n in ("q", "k", "v", "o"):
+                setattr(self, n, torch.nn.Linear(128, 128))
+
+    class Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.self_attn, self.cross_attn = Attn(), Attn()
+            self.ffn = torch.nn.Sequential(torch.nn.Linear(128, 256), torch.nn.GELU(),
+                                           torch.nn.Linear(256, 128))
+
+    class Model(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.blocks = torch.nn.ModuleList([Block() for _ in range(4)])
+            self.head = torch.nn.Linear(128, 16)
+
+    model = Model().to(torch.bfloat16).cuda()
+    names = convert_linears_to_fp8(model, skip_first=1, skip_last=1)
+    assert names == [f"blocks.{i}.{s}" for i in (1, 2) for s in TARGETS_ALL]
+    assert isinstance(model.blocks[1].ffn[2], Fp8Linear)
+    assert isinstance(model.blocks[0].ffn[0], torch.nn.Linear)
+    assert isinstance(model.head, torch.nn.Linear)
+    assert convert_linears_to_fp8(model, skip_first=1, skip_last=1) == []     # idempotent
+
+
+def test_quantise_and_gemm_replay_in_a_graph():
+    """Per-tensor quantiser (kernel-cleared workspace) + GEMM captured once and
+    replayed on changing inputs, eager work between replays, every replay checked."""
+    from sr_dit import fp8_linear as fl
+    torch.manual_seed(1)
+    lin = torch.nn.Linear(256, 512, bias=True).to(torch.bfloat16).cuda()
+    m = fl.Fp8Linear.from_linear(lin, scaling="tensor")
+    x = torch.randn(640, 256, dtype=torch.bfloat16, device="cuda")
+    m(x)                                      # allocate the workspace outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = m(x)
+    for it in range(4):
+        x.copy_(torch.randn(640, 256, dtype=torch.bfloat16, device="cuda") * (1 + 3 * it))
+        g.replay()
+        torch.cuda.synchronize()
+        want = m(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), it
