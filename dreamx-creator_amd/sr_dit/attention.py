@@ -353,8 +353,11 @@ def mask_free_window_attention(
                           else anchor_keep[i])
                 use_anchor = bool(keep_i)
 
-        bt = int(block_t if block_t is not None else
-                 (causal_chunk_frames if causal_chunk_frames is not None else 1))
+        if block_t is None and causal_chunk_frames is None:
+            # attention.py:1575 evaluates int(None) here and raises TypeError.
+            raise TypeError("mask_free_window_attention: block_t or causal_chunk_frames "
+                            "must be given for the block-grid path.")
+        bt = int(block_t if block_t is not None else causal_chunk_frames)
         if bt <= 0:
             raise ValueError(f"block_t must be positive, got {bt}.")
         is_streaming = (pre_cache_k is not None or pre_cache_v is not None or anchor_given)

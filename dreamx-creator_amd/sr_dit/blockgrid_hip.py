@@ -28,7 +28,7 @@ from . import _lib
 P_PLAIN = 19
 P_FRAME = 17
 
-#: Query rows handled by one wavefront of the HIP kernel (two 32-row MFMA tiles).
+#: Query rows per HIP workgroup: two wavefronts, one 32-row MFMA tile each.
 HIP_BLOCK_M = 64
 
 

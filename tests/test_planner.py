@@ -155,3 +155,13 @@ def test_useful_flops_factorise():
         assert obg.useful_flops(g) == 4 * 128 * 24 * st * sh * sw
     g = obg.Geometry(f_cur=6, f_kv=6, h=45, w=80, block_t=1, bh=8, bw=8, rh=1, rw=1, sym_rt=1)
     assert abs(obg.useful_flops(g) / 330.13e9 - 1) < 1e-4
+
+
+def test_op_needs_block_t_or_chunk_frames():
+    """attention.py:1575 takes int(None) when neither is given: a TypeError."""
+    import torch
+    from sr_dit import attention as att
+    q = torch.zeros(1, 768, 2, 128, dtype=torch.bfloat16)
+    grid = torch.tensor([[3, 16, 16]])
+    with pytest.raises(TypeError):
+        att.mask_free_window_attention(q, q, q, grid, block_hw=(8, 8), block_radius_hw=(1, 1))
