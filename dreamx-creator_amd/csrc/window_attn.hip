@@ -28,60 +28,12 @@
 // The exponential is evaluated as exp2 of log2(e)-scaled logits, and the
 // running max is refreshed lazily (see TAU).
 
-#include "common.h"
-
-#include <utility>
+#include "window_common.h"
 
 namespace srdit {
 namespace {
 
-// Unrolled loop with a compile-time index (DPP controls must be immediates).
-template <typename F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(std::integral_constant<int, Is>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
-
-// Eight fp32 values -> one 8-element MFMA operand, converted two at a time
-// (v_cvt_pk_*) and assembled as whole 32-bit registers.
-template <typename H2, typename V8>
-__device__ __forceinline__ V8 pack8_impl(const float* x) {
-  i32x4_t w;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const f32x2_t f = {x[2 * j], x[2 * j + 1]};
-    w[j] = __builtin_bit_cast(int, __builtin_convertvector(f, H2));
-  }
-  return __builtin_bit_cast(V8, w);
-}
-
-template <typename T> struct Elem;
-template <> struct Elem<__bf16> {
-  typedef bf16x8_t v8;
-  typedef bf16x2_t h2;
-  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<h2, v8>(x); }
-};
-template <> struct Elem<_Float16> {
-  typedef f16x8_t v8;
-  typedef f16x2_t h2;
-  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<h2, v8>(x); }
-};
+using namespace win;
 
 struct WinArgs {
   const void* q;
@@ -98,99 +50,8 @@ struct WinArgs {
 
 constexpr int WAVES = 2;  // wavefronts per workgroup, 32 queries each
 constexpr int KN = 32;    // keys per step
-constexpr int STAGES = 2; // LDS ring depth: the fill of step i+STAGES-1 overlaps step i
+constexpr int STAGES = 2; // LDS ring: the unrolled step pair alternates the two stages
 
-// Largest growth (log2 units) of a query's running max tolerated before the
-// accumulator is rescaled.  Between rescales P = exp2(s - m_used) <= 2^TAU,
-// which the final O = acc / l normalisation cancels exactly; it only bounds
-// the range (2^8 fits bf16 and fp16 P with room to spare).
-constexpr float TAU = 8.0f;
-
-// n / d for 0 <= n < 2^22, d > 0, rd = 1/d: float estimate plus one correction.
-__device__ __forceinline__ int fdiv(int n, int d, float rd) {
-  int qv = static_cast<int>(static_cast<float>(n) * rd);
-  const int r = n - qv * d;
-  qv += (r >= d) - (r < 0);
-  return qv;
-}
-
-__device__ __forceinline__ float other_half_max(float x) {
-  i32x2_t s = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-  return fmaxf(__int_as_float(s[0]), __int_as_float(s[1]));
-}
-__device__ __forceinline__ float half_sum(float x) {
-  i32x2_t s = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-  return __int_as_float(s[0]) + __int_as_float(s[1]);
-}
-
-// Compiler-only fence: keeps LDS/DMA accesses on their side of a wait or a
-// barrier without emitting any wait of its own.
-__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
-
-// All of this wavefront's memory operations (the DMA fills, the LDS reads)
-// retired, then a workgroup barrier: after it every fill issued before it by
-// either wavefront is in LDS, and every LDS read issued before it has returned.
-__device__ __forceinline__ void fill_barrier() {
-  compiler_fence();
-  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
-  __builtin_amdgcn_s_barrier();
-  compiler_fence();
-}
-
-// As fill_barrier, but the last `keep` vector-memory operations this wavefront
-// issued may still be in flight (vmcnt(keep)); LDS reads are all retired.
-template <int N>
-__device__ __forceinline__ void waitcnt_vm_keep() {
-  static_assert(N >= 0 && N < 64, "vmcnt out of range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // lgkmcnt(0)
-}
-__device__ __forceinline__ void fill_barrier_keep(int keep) {
-  compiler_fence();
-  switch (keep) {  // s_waitcnt takes an immediate
-    case 0: waitcnt_vm_keep<0>(); break;
-    case 4: waitcnt_vm_keep<4>(); break;
-    case 8: waitcnt_vm_keep<8>(); break;
-    case 12: waitcnt_vm_keep<12>(); break;
-    case 16: waitcnt_vm_keep<16>(); break;
-    default: waitcnt_vm_keep<0>(); break;
-  }
-  __builtin_amdgcn_s_barrier();
-  compiler_fence();
-}
-
-// One contiguous run of keys with a common decode:
-//   token = base + (t0 + j/sp)*frame_len + (r0 + (j%sp)/cols)*Wg + c0 + (j%sp)%cols
-// The HR cuboid, the anchor prefix of the plain kernel and an anchor segment of
-// the frame kernel are all this formula with their own grid.
-struct KeyRun {
-  int n;          // keys in the run
-  int base;       // token offset of frame 0 of the run
-  int frame_len;  // tokens per frame of the grid the run lives on
-  int t0, r0, c0; // first frame / row / column
-  int rows, cols; // cuboid rows / columns per frame
-  int Wg;         // grid width (row stride in tokens)
-  float r_sp, r_cols;
-};
-
-__device__ __forceinline__ KeyRun make_run(int n, int base, int frame_len, int t0, int r0,
-                                           int c0, int rows, int cols, int Wg) {
-  KeyRun k;
-  k.n = n; k.base = base; k.frame_len = frame_len; k.t0 = t0; k.r0 = r0; k.c0 = c0;
-  k.rows = rows; k.cols = cols; k.Wg = Wg;
-  k.r_sp = 1.0f / static_cast<float>(rows * cols);
-  k.r_cols = 1.0f / static_cast<float>(cols);
-  return k;
-}
-
-// Token index of key j of the run (token counts are below 2^31, checked on entry).
-__device__ __forceinline__ int run_token(const KeyRun& k, int j) {
-  const int sp = k.rows * k.cols;
-  const int t = fdiv(j, sp, k.r_sp);
-  const int rr = j - t * sp;
-  const int row = fdiv(rr, k.cols, k.r_cols);
-  const int col = rr - row * k.cols;
-  return k.base + (k.t0 + t) * k.frame_len + (k.r0 + row) * k.Wg + (k.c0 + col);
-}
 
 template <typename T, int D>
 struct Tile {
@@ -205,10 +66,18 @@ struct Tile {
   float mrun, lrun;    // running max (log2 units, lazily refreshed) and sum
 };
 
-// Walk one key run with the online softmax.  `seg` >= 0 restricts the run to
-// queries of frame `seg` (per-frame anchor), -1 admits all.  Must be called
-// by both wavefronts of the workgroup with the same run (barriers inside).
-//
+// Per-lane LDS byte offsets, loop-invariant: the K A-operand reads, the V^T
+// transposing reads (lane part; the key-block part is a compile-time constant)
+// and the 16-byte chunk each fill load of this wavefront reads from its key's
+// head row (K swizzle for wavefront 0, V swizzle for wavefront 1).
+template <int D>
+struct LaneOff {
+  static constexpr int KS = D / 16, DT = D / 32, NL = D / 16;
+  int k[KS];
+  int v[DT];
+  int fill[NL];
+};
+
 // LDS tiles: 32 keys x D, one row of CPK 16-byte slots per key (chunk L = 8
 // head dims), row-major with an XOR swizzle of the slot within its row:
 //   slot(key, L) = key*CPK + (L ^ swz(key)).
@@ -218,11 +87,80 @@ struct Tile {
 // 64/CPK full rows.  The swizzles (K: (key*CPK/16) % CPK; V: for D=128
 // 4(key%4) ^ 8((key>>2)&1), for D=64 key%8) make the K A-operand reads and the
 // V transposing reads hit every bank group equally often.
+template <int D> __device__ __forceinline__ int swz_k(int key) { return (key * (D / 8) / 16) % (D / 8); }
+template <int D> __device__ __forceinline__ int swz_v(int key) {
+  return D == 128 ? ((4 * (key & 3)) ^ (8 * ((key >> 2) & 1))) : (key % (D / 8));
+}
+
+template <int D>
+__device__ __forceinline__ LaneOff<D> make_lane_offsets(int wave) {
+  constexpr int CPK = D / 8, LPK = CPK, KPI = 64 / CPK;
+  LaneOff<D> o;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 31, hf = lane >> 5;
+  const int g = lane >> 4, i16 = lane & 15;
+#pragma unroll
+  for (int ks = 0; ks < LaneOff<D>::KS; ++ks)
+    o.k[ks] = (c * CPK + ((hf * LaneOff<D>::KS + ks) ^ swz_k<D>(c))) * 16;
+  // V^T read of (kk, dt, h2): key = 16kk + 8h2 + kl with kl = 4hf + i16/4; the
+  // swizzle of such a key depends on kl only, so the lane part is
+  // (kl*CPK + (Lc ^ swz_v(kl)))*16 + 8*(i16&1) and 16kk + 8h2 adds rows.
+  const int kl = 4 * hf + (i16 >> 2);
+#pragma unroll
+  for (int dt = 0; dt < LaneOff<D>::DT; ++dt) {
+    const int Lc = 4 * dt + 2 * (g & 1) + ((i16 & 3) >> 1);
+    o.v[dt] = (kl * CPK + (Lc ^ swz_v<D>(kl))) * 16 + 8 * (i16 & 1);
+  }
+  const int sub = (lane & 15) / LPK, pos = lane % CPK;
+#pragma unroll
+  for (int q = 0; q < LaneOff<D>::NL; ++q) {
+    const int key = q * KPI + (lane >> 4) * (16 / LPK) + sub;
+    o.fill[q] = (pos ^ (wave == 0 ? swz_k<D>(key) : swz_v<D>(key))) * 16;
+  }
+  return o;
+}
+
+// Token of key j of a run, walked forward KN keys per step: the lane keeps its
+// key's index within the current frame and that frame's first token.
+struct KeyCursor {
+  int rr;         // index of the key within its frame of the run
+  int frame_tok;  // token of that frame's first cuboid cell: base + (t0+t)*frame_len
+};
+
+__device__ __forceinline__ KeyCursor cursor_at(const KeyRun& k, int j) {
+  const int sp = k.rows * k.cols;
+  const int t = fdiv(j, sp, k.r_sp);
+  KeyCursor c;
+  c.rr = j - t * sp;
+  c.frame_tok = k.base + (k.t0 + t) * k.frame_len;
+  return c;
+}
+
+__device__ __forceinline__ int cursor_token(const KeyRun& k, const KeyCursor& c) {
+  const int row = fdiv(c.rr, k.cols, k.r_cols);
+  const int col = c.rr - row * k.cols;
+  return c.frame_tok + __mul24(k.r0 + row, k.Wg) + (k.c0 + col);
+}
+
+__device__ __forceinline__ void cursor_advance(const KeyRun& k, KeyCursor& c, int by) {
+  const int sp = k.rows * k.cols;
+  c.rr += by;
+  while (c.rr >= sp) {  // at most ceil(by / sp) frames
+    c.rr -= sp;
+    c.frame_tok += k.frame_len;
+  }
+}
+
+// Walk one key run with the online softmax.  `seg` >= 0 restricts the run to
+// queries of frame `seg` (per-frame anchor), -1 admits all.  Must be called
+// by both wavefronts of the workgroup with the same run (barriers inside).
+// `kvrsrc` is a structured buffer over this head's K (wavefront 0) or V
+// (wavefront 1): record = token, stride = token stride in bytes.
 template <typename T, int D>
 __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, int seg, int wave,
                                            int qframe, bool qvalid, __amdgpu_buffer_rsrc_t kvrsrc,
-                                           int tok_bytes, int kv_tokens, float scale_log2,
-                                           T* ksh, T* vsh) {
+                                           int kv_tokens, float scale_log2, T* ksh, T* vsh,
+                                           const LaneOff<D>& lo) {
   using TT = Tile<T, D>;
   using E = typename TT::E;
   using V8 = typename TT::V8;
@@ -231,30 +169,28 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
   constexpr int CPK = D / 8;    // 16-byte chunks per key row
   constexpr int LPK = CPK;      // fill lanes per key row
   constexpr int KPI = 64 / CPK; // key rows per fill load
-  auto swz_k = [](int key) { return (key * CPK / 16) % CPK; };
-  auto swz_v = [](int key) {
-    return D == 128 ? ((4 * (key & 3)) ^ (8 * ((key >> 2) & 1))) : (key % CPK);
-  };
   if (run.n <= 0) return;
   const int lane = threadIdx.x & 63;
-  const int c = lane & 31, hf = lane >> 5;
-  const int g = lane >> 4, i16 = lane & 15;
+  const int hf = lane >> 5;
   const int nsteps = (run.n + KN - 1) / KN;
   const bool admit = (seg < 0) || (qvalid && qframe == seg);
 
   // Fill of step i into stage i & 1: wavefront 0 loads K, wavefront 1 loads V.
-  // The token of each key row is decoded once per step by a source lane and
-  // broadcast to the row's lanes with DPP row_newbcast: source lane s of a
-  // 16-lane row r holds the key that load (s % LPK) places in that row's
-  // sub-row s / LPK.
-  auto fill = [&](int i) {
-    const int s = lane & 15;
-    const int src_key = (s % LPK) * KPI + (lane >> 4) * (16 / LPK) + s / LPK;
-    const int j = i * KN + src_key;
-    int tokv = run_token(run, j < run.n ? j : run.n - 1);
+  // Source lane s of a 16-lane row r holds the token of the key that load
+  // (s % LPK) places in that row's sub-row s / LPK; DPP row_newbcast hands it
+  // to the row's lanes.  The lane's key advances KN keys per step.
+  const int s16 = lane & 15;
+  const int src_key = (s16 % LPK) * KPI + (lane >> 4) * (16 / LPK) + s16 / LPK;
+  KeyCursor cur = cursor_at(run, src_key < run.n ? src_key : run.n - 1);
+  int fill_key = src_key;
+  const int sub = s16 / LPK;
+  T* const fill_base = wave == 0 ? ksh : vsh;
+  auto fill = [&](int stage) {  // stage is a constant after inlining
+    int tokv = cursor_token(run, cur);
     tokv = tokv < 0 ? 0 : (tokv >= kv_tokens ? kv_tokens - 1 : tokv);
-    T* dst = (wave == 0 ? ksh : vsh) + (i % STAGES) * TILE;
-    const int sub = s / LPK, pos = lane % CPK;
+    // keys past the run are clamped tokens; their scores are masked
+    fill_key += KN;
+    if (fill_key < run.n) cursor_advance(run, cur, KN);
     static_for<NL>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       int t = __builtin_amdgcn_mov_dpp(tokv, 0x150 + q, 0xf, 0xf, false);
@@ -262,34 +198,25 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
         const int t1 = __builtin_amdgcn_mov_dpp(tokv, 0x150 + 8 + q, 0xf, 0xf, false);
         t = sub ? t1 : t;
       }
-      // byte offset of this lane's 16-byte chunk: lane-constant per q
-      const int key = q * KPI + (lane >> 4) * (16 / LPK) + sub;
-      const int chunk_off = (pos ^ (wave == 0 ? swz_k(key) : swz_v(key))) * 16;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          kvrsrc, (lds_void_t*)(dst + q * 512), 16,
-          static_cast<int>(__umul24(t, tok_bytes)) + chunk_off, 0, 0, 0);
+      buffer_load_lds_x4(kvrsrc, fill_base + stage * TILE + q * 512, t, lo.fill[q]);
     });
   };
 
-  // Fills run STAGES-1 steps ahead.  The wait at the top of step i leaves the
-  // fills of steps i+1 .. i+STAGES-2 in flight (one group of NL loads each).
-#pragma unroll
-  for (int f = 0; f < STAGES - 1; ++f)
-    if (f < nsteps) fill(f);
-  for (int i = 0; i < nsteps; ++i) {
+  // One step on stage `stage` (a compile-time constant, so every LDS address
+  // below is a lane offset plus an immediate).
+  auto step = [&](int i, auto stage_c) {
+    constexpr int stage = decltype(stage_c)::value;
     // Fill i has landed in both halves and step i-1's LDS reads are done, so
-    // stage (i + STAGES - 1) % STAGES (step i-1's) may be refilled.
-    const int ahead = nsteps - 1 - i < STAGES - 2 ? nsteps - 1 - i : STAGES - 2;
-    fill_barrier_keep(ahead * NL);
-    if (i + STAGES - 1 < nsteps) fill(i + STAGES - 1);
-    const T* kbuf = ksh + (i % STAGES) * TILE;
-    const T* vbuf = vsh + (i % STAGES) * TILE;
+    // the other stage (step i-1's) may be refilled with step i+1.
+    fill_barrier();
+    if (i + 1 < nsteps) fill(stage ^ 1);
+    const char* kbuf = reinterpret_cast<const char*>(ksh + stage * TILE);
+    const char* vbuf = reinterpret_cast<const char*>(vsh + stage * TILE);
 
     // S^T = K Q^T: all K fragments of the step first, then the MFMA chain
     V8 kf[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      kf[ks] = *reinterpret_cast<const V8*>(kbuf + (c * CPK + ((hf * KS + ks) ^ swz_k(c))) * 8);
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const V8*>(kbuf + lo.k[ks]);
     f32x16_t sacc = f32x16_t{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) sacc = E::mma(kf[ks], st.qf[ks], sacc);
@@ -334,22 +261,19 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
     const V8 pf0 = E::pack8(&pv[0]);
     const V8 pf1 = E::pack8(&pv[8]);
 
-    // O^T += V^T P^T, V^T via transposing LDS reads: the lane reads 8 bytes of
-    // chunk L = 4dt + 2(g&1) + (i16&3)/2, half (i16&1), of key 16kk + 8h2 +
-    // 4hf + i16/4, and receives four consecutive keys of head dim dt*32 + c.
+    // O^T += V^T P^T, V^T via transposing LDS reads: the lane receives four
+    // consecutive keys (16kk + 8h2 + 4hf + i16/4 ...) of head dim dt*32 + c.
     V8 vt[2][DT];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const int L = 4 * dt + 2 * (g & 1) + ((i16 & 3) >> 1);
         i32x2_t half[2];
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
-          const int key = 16 * kk + 8 * h2 + 4 * hf + (i16 >> 2);
-          const T* src = vbuf + (key * CPK + (L ^ swz_v(key))) * 8 + 4 * (i16 & 1);
+          const char* src = vbuf + (16 * kk + 8 * h2) * CPK * 16 + lo.v[dt];
           half[h2] = __builtin_bit_cast(
-              i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(const_cast<T*>(src))));
+              i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(const_cast<char*>(src))));
         }
         const i32x4_t vw = {half[0][0], half[0][1], half[1][0], half[1][1]};
         vt[kk][dt] = __builtin_bit_cast(V8, vw);
@@ -359,7 +283,15 @@ __device__ __forceinline__ void attend_run(Tile<T, D>& st, const KeyRun& run, in
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) st.oacc[dt] = E::mma(vt[kk][dt], kk == 0 ? pf0 : pf1, st.oacc[dt]);
+  };
+
+  fill(0);
+  int i = 0;
+  for (; i + 1 < nsteps; i += 2) {
+    step(i, std::integral_constant<int, 0>{});
+    step(i + 1, std::integral_constant<int, 1>{});
   }
+  if (i < nsteps) step(i, std::integral_constant<int, 0>{});
   fill_barrier();  // stages free for the next run
 }
 
@@ -409,13 +341,14 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
   const int L = a.H * a.W;
   const int64_t tok = static_cast<int64_t>(a.n_heads) * D;
   const T* qb = reinterpret_cast<const T*>(a.q) + head * D;
-  // K (wavefront 0) or V (wavefront 1) of this head as a buffer resource:
-  // 32-bit byte offsets, hardware range check against the whole tensor.
+  // K (wavefront 0) or V (wavefront 1) of this head as a structured buffer:
+  // record = token, stride = token stride in bytes; the hardware checks the
+  // record index against kv_tokens.
   const int tok_bytes = static_cast<int>(tok) * static_cast<int>(sizeof(T));
   const T* kvb = reinterpret_cast<const T*>(wave == 0 ? a.k : a.v) + head * D;
   const __amdgpu_buffer_rsrc_t kvrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<T*>(kvb), 0, static_cast<int>(a.kv_tokens) * tok_bytes - head * D * static_cast<int>(sizeof(T)),
-      0x00020000);
+      const_cast<T*>(kvb), static_cast<short>(tok_bytes), static_cast<int>(a.kv_tokens), 0x00020000);
+  const LaneOff<D> lo = make_lane_offsets<D>(wave);
   const int kv_tokens = static_cast<int>(a.kv_tokens);
   T* ob = reinterpret_cast<T*>(a.o) + head * D;
 
@@ -449,13 +382,13 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
     // anchor prefix (a_frames whole-chunk anchor frames), then the HR cuboid
     if (a_frames > 0 && anchor_ok) {
       KeyRun ar = make_run(a_frames * sp_a, 0, h_a * w_a, 0, kh0_a, kw0_a, kh_l_a, kw_l_a, w_a);
-      attend_run<T, D>(st, ar, -1, wave, qframe, qvalid, kvrsrc, tok_bytes, kv_tokens, a.scale_log2,
-                       ksh, vsh);
+      attend_run<T, D>(st, ar, -1, wave, qframe, qvalid, kvrsrc, kv_tokens, a.scale_log2,
+                       ksh, vsh, lo);
     }
     if (sp_hr > 0 && kv_tl > 0) {
       KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
-      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kvrsrc, tok_bytes, kv_tokens, a.scale_log2,
-                       ksh, vsh);
+      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kvrsrc, kv_tokens, a.scale_log2,
+                       ksh, vsh, lo);
     }
   } else {
     // per-frame anchor: query frame s sees anchor frame s only, over the
@@ -466,14 +399,14 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
       for (int s = f_lo; s <= f_hi; ++s) {
         KeyRun ar = make_run(sp_a, s * h_a * w_a, h_a * w_a, 0, kh0_a, kw0_a,
                              kh_l_a, kw_l_a, w_a);
-        attend_run<T, D>(st, ar, s, wave, qframe, qvalid, kvrsrc, tok_bytes, kv_tokens, a.scale_log2,
-                         ksh, vsh);
+        attend_run<T, D>(st, ar, s, wave, qframe, qvalid, kvrsrc, kv_tokens, a.scale_log2,
+                         ksh, vsh, lo);
       }
     }
     if (sp_hr > 0 && kv_tl > 0) {
       KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
-      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kvrsrc, tok_bytes, kv_tokens, a.scale_log2,
-                       ksh, vsh);
+      attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kvrsrc, kv_tokens, a.scale_log2,
+                       ksh, vsh, lo);
     }
   }
 
@@ -528,8 +461,9 @@ extern "C" int srdit_window_attn_fwd(const void* q, const void* k, const void* v
   SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 22), "srdit_window_attn_fwd: grid too large");
   SRDIT_REQUIRE(kv_tokens * n_heads * head_dim * 2 < (1LL << 31) && q_tokens < (1LL << 24),
                 "srdit_window_attn_fwd: K/V must span fewer than 2^31 bytes and 2^24 tokens");
-  SRDIT_REQUIRE(static_cast<int64_t>(n_heads) * head_dim * 2 < (1LL << 24),
-                "srdit_window_attn_fwd: token stride too large");
+  SRDIT_REQUIRE(static_cast<int64_t>(n_heads) * head_dim * 2 < (1LL << 14),
+                "srdit_window_attn_fwd: token stride n_heads*head_dim*2 must be below 16384 bytes "
+                "(structured-buffer stride)");
   if (head_dim != 64 && head_dim != 128) {
     set_error("srdit_window_attn_fwd: head_dim %d unsupported (64 or 128)", head_dim);
     return SRDIT_EUNSUPPORTED;

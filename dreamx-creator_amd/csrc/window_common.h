@@ -1,0 +1,170 @@
+// Device helpers shared by the window-attention kernels (gfx950).
+#pragma once
+
+#include "common.h"
+
+#include <utility>
+
+namespace srdit {
+namespace win {
+
+// Unrolled loop with a compile-time index (DPP controls must be immediates).
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+// Eight fp32 values -> one 8-element MFMA operand, converted two at a time
+// (v_cvt_pk_*) and assembled as whole 32-bit registers.
+template <typename H2, typename V8>
+__device__ __forceinline__ V8 pack8_impl(const float* x) {
+  i32x4_t w;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const f32x2_t f = {x[2 * j], x[2 * j + 1]};
+    w[j] = __builtin_bit_cast(int, __builtin_convertvector(f, H2));
+  }
+  return __builtin_bit_cast(V8, w);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<__bf16> {
+  typedef bf16x8_t v8;
+  typedef bf16x2_t h2;
+  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<h2, v8>(x); }
+};
+template <> struct Elem<_Float16> {
+  typedef f16x8_t v8;
+  typedef f16x2_t h2;
+  static __device__ __forceinline__ f32x16_t mma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<h2, v8>(x); }
+};
+
+// Largest growth (log2 units) of a query's running max tolerated before the
+// accumulator is rescaled.  Between rescales P = exp2(s - m_used) <= 2^TAU,
+// which the final O = acc / l normalisation cancels exactly; it only bounds
+// the range (2^8 fits bf16 and fp16 P with room to spare).
+constexpr float TAU = 8.0f;
+
+// n / d for 0 <= n < 2^22, d > 0, rd = 1/d: float estimate plus one correction
+// (the estimate is within one of n / d, so qv * d stays below 2^23 and fits the
+// 24-bit multiply).
+__device__ __forceinline__ int fdiv(int n, int d, float rd) {
+  int qv = static_cast<int>(static_cast<float>(n) * rd);
+  const int r = n - __mul24(qv, d);
+  qv += (r >= d) - (r < 0);
+  return qv;
+}
+
+__device__ __forceinline__ float other_half_max(float x) {
+  i32x2_t s = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(__int_as_float(s[0]), __int_as_float(s[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  i32x2_t s = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return __int_as_float(s[0]) + __int_as_float(s[1]);
+}
+
+// 16 bytes per lane from record `index`, byte `offset` of a structured buffer
+// straight into LDS at lds + 16 * lane (buffer_load_dwordx4 ... idxen offen lds).
+// A plain device function: the builtin is a device-only one, and a template
+// instantiated in the host pass must not name it.
+__device__ __forceinline__ void buffer_load_lds_x4(__amdgpu_buffer_rsrc_t rsrc, void* lds, int index,
+                                                   int offset) {
+  __builtin_amdgcn_struct_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)lds, 16, index, offset, 0, 0, 0);
+}
+
+// Compiler-only fence: keeps LDS/DMA accesses on their side of a wait or a
+// barrier without emitting any wait of its own.
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// All of this wavefront's memory operations (the DMA fills, the LDS reads)
+// retired, then a workgroup barrier: after it every fill issued before it by
+// either wavefront is in LDS, and every LDS read issued before it has returned.
+__device__ __forceinline__ void fill_barrier() {
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  compiler_fence();
+}
+
+// As fill_barrier, but the last `keep` vector-memory operations this wavefront
+// issued may still be in flight (vmcnt(keep)); LDS reads are all retired.
+template <int N>
+__device__ __forceinline__ void waitcnt_vm_keep() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // lgkmcnt(0)
+}
+__device__ __forceinline__ void fill_barrier_keep(int keep) {
+  compiler_fence();
+  switch (keep) {  // s_waitcnt takes an immediate; keep counts whole load groups
+    case 0: waitcnt_vm_keep<0>(); break;
+    case 4: waitcnt_vm_keep<4>(); break;
+    case 8: waitcnt_vm_keep<8>(); break;
+    case 12: waitcnt_vm_keep<12>(); break;
+    case 16: waitcnt_vm_keep<16>(); break;
+    case 24: waitcnt_vm_keep<24>(); break;
+    case 32: waitcnt_vm_keep<32>(); break;
+    case 40: waitcnt_vm_keep<40>(); break;
+    case 48: waitcnt_vm_keep<48>(); break;
+    case 56: waitcnt_vm_keep<56>(); break;
+    default: waitcnt_vm_keep<0>(); break;  // any other count: wait for everything
+  }
+  __builtin_amdgcn_s_barrier();
+  compiler_fence();
+}
+
+// One contiguous run of keys with a common decode:
+//   token = base + (t0 + j/sp)*frame_len + (r0 + (j%sp)/cols)*Wg + c0 + (j%sp)%cols
+// The HR cuboid, the anchor prefix of the plain kernel and an anchor segment of
+// the frame kernel are all this formula with their own grid.
+struct KeyRun {
+  int n;          // keys in the run
+  int base;       // token offset of frame 0 of the run
+  int frame_len;  // tokens per frame of the grid the run lives on
+  int t0, r0, c0; // first frame / row / column
+  int rows, cols; // cuboid rows / columns per frame
+  int Wg;         // grid width (row stride in tokens)
+  float r_sp, r_cols;
+};
+
+__device__ __forceinline__ KeyRun make_run(int n, int base, int frame_len, int t0, int r0,
+                                           int c0, int rows, int cols, int Wg) {
+  KeyRun k;
+  k.n = n; k.base = base; k.frame_len = frame_len; k.t0 = t0; k.r0 = r0; k.c0 = c0;
+  k.rows = rows; k.cols = cols; k.Wg = Wg;
+  k.r_sp = 1.0f / static_cast<float>(rows * cols);
+  k.r_cols = 1.0f / static_cast<float>(cols);
+  return k;
+}
+
+// Token index of key j of the run (token counts are below 2^31, checked on entry).
+__device__ __forceinline__ int run_token(const KeyRun& k, int j) {
+  const int sp = k.rows * k.cols;
+  const int t = fdiv(j, sp, k.r_sp);
+  const int rr = j - t * sp;
+  const int row = fdiv(rr, k.cols, k.r_cols);
+  const int col = rr - row * k.cols;
+  return k.base + (k.t0 + t) * k.frame_len + (k.r0 + row) * k.Wg + (k.c0 + col);
+}
+
+
+}  // namespace win
+}  // namespace srdit

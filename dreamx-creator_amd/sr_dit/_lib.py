@@ -25,6 +25,9 @@ SIGNATURES = {
                                        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                        _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_int,
                                        _c_int, _c_p]),
+    "srdit_window_attn_grouped_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int,
+                                               _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_int,
+                                               _c_int, _c_f, _c_int, _c_p]),
     "srdit_fp8_quant_rowwise": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p]),
     "srdit_fp8_quant_tensor": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
                                         _c_p]),
@@ -84,6 +87,17 @@ def window_attn_fwd(q, k, v, o, params, order, *, n_w, m_tiles, p_stride, hr_bas
         int(q.shape[0]), int(kv_tokens), int(n_heads), int(head_dim), float(scale),
         int(mode), DTYPE_CODES[q.dtype], _stream(q.device))
     _check(rc, "srdit_window_attn_fwd")
+
+
+def window_attn_grouped_fwd(q, k, v, o, params, groups, *, n_w, n_groups, hr_base, H, W,
+                            n_heads, head_dim, kv_tokens, scale):
+    if q.dtype not in DTYPE_CODES:
+        raise ValueError(f"window attention needs bf16 or fp16, got {q.dtype}")
+    rc = load().srdit_window_attn_grouped_fwd(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(params), _ptr(groups),
+        int(n_w), int(n_groups), int(hr_base), int(H), int(W), int(q.shape[0]), int(kv_tokens),
+        int(n_heads), int(head_dim), float(scale), DTYPE_CODES[q.dtype], _stream(q.device))
+    _check(rc, "srdit_window_attn_grouped_fwd")
 
 
 QUANT_DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

@@ -165,6 +165,66 @@ def longest_first_order(plan) -> torch.Tensor:
     return torch.tensor(order, dtype=torch.int32)
 
 
+def groups_supported(plan) -> bool:
+    """True when the grouped kernel can run the plan: plain rows, no anchor prefix."""
+    if plan["p_stride"] != P_PLAIN:
+        return False
+    return bool((plan["params"][:, 12] == 0).all())
+
+
+def build_groups(plan) -> torch.Tensor:
+    """Pair the plan's 64-query members for the grouped kernel; int32 [G, 4].
+
+    A member is (row, m-tile) for every 64-row tile of a window's queries.  The
+    m-tiles of one window pair with each other (identical KV).  Remaining
+    members pair with the next member, in frame order, whose window has the
+    same spatial KV extent (kh0, khL, kw0, kwL) and an overlapping frame range
+    (the neighbouring query frames of the +-1-frame and streaming rules); those
+    pairs share the K/V fetches of their common frames.  Unpaired members run
+    alone (row1 = -1).  Groups are ordered by their first member's row, the
+    planner's raster order.
+    """
+    p = plan["params"].tolist()
+    singles = []
+    groups = []
+    for r, row in enumerate(p):
+        lq = row[1] * row[4] * row[5]
+        tiles = list(range(-(-lq // HIP_BLOCK_M))) if lq > 0 else []
+        while len(tiles) >= 2:
+            groups.append((r, tiles[0], r, tiles[1]))
+            tiles = tiles[2:]
+        if tiles:
+            singles.append((r, tiles[0]))
+    buckets: dict = {}
+    for r, mt in singles:
+        row = p[r]
+        buckets.setdefault((row[8], row[9], row[10], row[11]), []).append((row[6], r, mt))
+    for lst in buckets.values():
+        lst.sort()
+        i = 0
+        while i < len(lst):
+            a0, r0, m0 = lst[i]
+            if i + 1 < len(lst):
+                a1, r1, m1 = lst[i + 1]
+                if min(a0 + p[r0][7], a1 + p[r1][7]) > max(a0, a1):
+                    groups.append((r0, m0, r1, m1))
+                    i += 2
+                    continue
+            groups.append((r0, m0, -1, 0))
+            i += 1
+    groups.sort(key=lambda g: (g[0], g[1]))
+    return torch.tensor(groups, dtype=torch.int32).reshape(-1, 4).contiguous()
+
+
+def paired_fraction(groups: torch.Tensor) -> float:
+    """Fraction of members that share a workgroup with a partner."""
+    n = groups.shape[0]
+    if n == 0:
+        return 0.0
+    paired = int((groups[:, 2] >= 0).sum())
+    return 2 * paired / (2 * paired + (n - paired))
+
+
 def _device_tables(plan, device):
     """(params, order) on ``device``, copied once per plan and device."""
     key = ("dev", device)
@@ -177,7 +237,7 @@ def _device_tables(plan, device):
 
 
 def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
-                      anchor_mode=None):
+                      anchor_mode=None, kernel="auto"):
     """Launch the fused window kernel for one sample; writes ``out`` and returns it.
 
     ``q``/``out``: ``[f_cur*h*w, n, d]``.  ``k_ext``/``v_ext``: the extended KV,
@@ -185,6 +245,13 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     anchor first), else the HR KV alone.  All four must be contiguous with a
     stride-1 head dim, on one device, bf16 or fp16.  The launch is
     asynchronous on the current stream.
+
+    ``kernel``: ``"auto"`` and ``"single"`` run the single-window kernel (two
+    32-query wavefronts per 64-query tile, two wavefronts per SIMD), the
+    faster one on every measured geometry; ``"grouped"`` runs the grouped
+    kernel (one 64-query member per wavefront, K/V fetches shared by paired
+    members), which needs plain rows without an anchor prefix and raises
+    otherwise.
     """
     for name, t in (("q", q), ("k_ext", k_ext), ("v_ext", v_ext), ("out", out)):
         if not t.is_cuda:
@@ -204,6 +271,21 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     mode = 1 if anchor_mode == "frame" else 0
     if (plan["p_stride"] == P_FRAME) != (mode == 1):
         raise ValueError("run_blockgrid_hip: plan layout does not match anchor_mode.")
+    if kernel not in ("auto", "grouped", "single"):
+        raise ValueError(f"run_blockgrid_hip: kernel must be auto, grouped or single, got {kernel!r}")
+    use_grouped = kernel == "grouped"
+    if use_grouped and not groups_supported(plan):
+        raise ValueError("run_blockgrid_hip: the grouped kernel needs plain rows without an anchor.")
+    if use_grouped:
+        key = ("groups", q.device)
+        groups = plan.get(key)
+        if groups is None:
+            groups = plan[key] = build_groups(plan).to(q.device)
+        _lib.window_attn_grouped_fwd(
+            q, k_ext, v_ext, out, params, groups, n_w=plan["n_w"], n_groups=groups.shape[0],
+            hr_base=hr_base, H=h, W=w, n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0],
+            scale=d ** -0.5)
+        return out
     _lib.window_attn_fwd(
         q, k_ext, v_ext, out, params, order,
         n_w=plan["n_w"], m_tiles=kernel_m_tiles(plan), p_stride=plan["p_stride"],

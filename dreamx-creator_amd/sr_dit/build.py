@@ -24,11 +24,12 @@ ARCH = "gfx950"
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-command-line-argument"]
-# Per-source additions.  The window kernel keeps its MFMA results and
-# accumulators in the VGPR form: its lazily rescaled O accumulator is otherwise
+# Per-source additions.  The window kernels keep their MFMA results and
+# accumulators in the VGPR form: a lazily rescaled O accumulator is otherwise
 # mirrored between AGPRs and VGPRs every step.  The GEMM needs the AGPRs for its
 # 256 accumulator registers per lane, so it keeps the default.
-FILE_FLAGS = {"window_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+FILE_FLAGS = {"window_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+              "window_group.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc() -> str:

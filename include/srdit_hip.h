@@ -58,6 +58,26 @@ int srdit_window_attn_fwd(const void* q, const void* k, const void* v, void* o,
                           int dtype, void* stream);
 
 /*
+ * Block-grid window attention, forward, plain windows without an anchor prefix,
+ * two 64-query members per workgroup sharing their K/V fetches.
+ *
+ * Replaces the same launch as srdit_window_attn_fwd mode 0
+ * (run_blockgrid_triton -> _blockgrid_fused_kernel, blockgrid_triton.py:392-422,
+ * :184-278) for tables whose rows all have a_frames == 0.
+ *
+ * params      int32 [n_w, 19] device table (the planner's plain rows)
+ * groups      int32 [n_groups, 4] device table: row0, m_tile0, row1, m_tile1;
+ *             row1 = -1 for a single member.  Paired rows must have the same
+ *             spatial KV extent (kh0, khL, kw0, kwL); m-tiles are 64 query rows.
+ * Other arguments as srdit_window_attn_fwd.
+ */
+int srdit_window_attn_grouped_fwd(const void* q, const void* k, const void* v, void* o,
+                                  const int32_t* params, const int32_t* groups,
+                                  int n_w, int n_groups, int hr_base, int H, int W,
+                                  int64_t q_tokens, int64_t kv_tokens, int n_heads,
+                                  int head_dim, float scale, int dtype, void* stream);
+
+/*
  * Row-wise fp8 e4m3 quantiser: for each row of x [M, K] (row stride ldx),
  *   scale[m] = max(amax(|x[m,:]|) * fl32(1/448), 1e-12)   (fp32; what torch computes
  *              for amax / 448.0 on a GPU tensor)

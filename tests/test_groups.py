@@ -1,0 +1,97 @@
+"""Grouped window kernel: host pairing of 64-query members and the slot schedule (CPU)."""
+import itertools
+
+import pytest
+
+from sr_dit import blockgrid_hip as bgh
+from sr_dit import workloads as wl
+
+
+def _members(plan):
+    out = set()
+    for r, row in enumerate(plan["params"].tolist()):
+        lq = row[1] * row[4] * row[5]
+        out |= {(r, mt) for mt in range(-(-lq // 64))}
+    return out
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2", "c3", "c4"])
+def test_groups_cover_every_member_once(cfg):
+    plan = bgh.build_plan(wl.window_spec(cfg))
+    g = bgh.build_groups(plan).tolist()
+    seen = []
+    p = plan["params"].tolist()
+    for r0, m0, r1, m1 in g:
+        seen.append((r0, m0))
+        if r1 >= 0:
+            seen.append((r1, m1))
+            assert p[r0][8:12] == p[r1][8:12]                       # same spatial KV extent
+            a0, la, a1, lb = p[r0][6], p[r0][7], p[r1][6], p[r1][7]
+            assert min(a0 + la, a1 + lb) > max(a0, a1)              # overlapping frames
+    assert len(seen) == len(set(seen)) and set(seen) == _members(plan)
+
+
+def test_c3_pairs_neighbouring_query_frames():
+    plan = bgh.build_plan(wl.window_spec("c3"))
+    p = plan["params"].tolist()
+    pairs = {(p[r0][0], p[r1][0]) for r0, _, r1, _ in bgh.build_groups(plan).tolist()}
+    assert pairs == {(0, 1), (2, 3), (4, 5)}
+
+
+def test_c4_pairs_the_two_m_tiles_of_each_window():
+    plan = bgh.build_plan(wl.window_spec("c4"))
+    g = bgh.build_groups(plan).tolist()
+    assert all(r0 == r1 and (m0, m1) == (0, 1) for r0, m0, r1, m1 in g)
+    assert len(g) == plan["n_w"]
+
+
+def _schedule(a0, la, a1, lb):
+    """Frame consumed by each member in each frame slot, as the kernel walks them:
+    private slots first (each member its own frames, in order), then shared frames."""
+    s_lo = max(a0, a1)
+    nsh = max(0, min(a0 + la, a1 + lb) - s_lo) if lb > 0 else 0
+
+    def priv(a, l):
+        if nsh == 0:
+            return list(range(a, a + l))
+        return list(range(a, min(a + l, s_lo))) + list(range(max(a, s_lo + nsh), a + l))
+
+    p0, p1 = priv(a0, la), priv(a1, lb) if lb > 0 else []
+    P = max(len(p0), len(p1))
+    slots = []
+    for k in range(P):
+        slots.append((p0[k] if k < len(p0) else None, p1[k] if k < len(p1) else None, 2))
+    for k in range(nsh):
+        slots.append((s_lo + k, s_lo + k, 1))
+    return slots
+
+
+def test_slot_schedule_consumes_each_frame_once():
+    for a0, la, a1, lb in itertools.product(range(4), range(1, 5), range(4), range(0, 5)):
+        slots = _schedule(a0, la, a1, lb)
+        f0 = [s[0] for s in slots if s[0] is not None]
+        f1 = [s[1] for s in slots if s[1] is not None]
+        assert sorted(f0) == list(range(a0, a0 + la))
+        assert sorted(f1) == list(range(a1, a1 + lb))
+        # a shared slot fetches one block that both members consume
+        assert all(s[0] == s[1] for s in slots if s[2] == 1)
+
+
+def test_grouping_cuts_c3_fetches():
+    """Blocks fetched per spatial step: c3's pairs fetch 10 frame blocks per window
+    column where single windows would fetch 16."""
+    plan = bgh.build_plan(wl.window_spec("c3"))
+    p = plan["params"].tolist()
+    single = sum(row[7] for row in p)
+    grouped = 0
+    for r0, _, r1, _ in bgh.build_groups(plan).tolist():
+        slots = _schedule(p[r0][6], p[r0][7], p[r1][6], p[r1][7])
+        grouped += sum((s[0] is not None) + (s[1] is not None) if s[2] == 2 else 1 for s in slots)
+    assert grouped * 16 == single * 10
+
+
+def test_unsupported_plans_and_kernel_switch():
+    spec = wl.window_spec("c1")
+    plan = bgh.build_plan(spec, anchor_mode="chunk")
+    assert not bgh.groups_supported(plan)
+    assert bgh.groups_supported(bgh.build_plan(spec))

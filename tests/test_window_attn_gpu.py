@@ -222,3 +222,56 @@ def test_raise_paths():
     with pytest.raises(ValueError):
         att.mask_free_window_attention(q.to(DEV).float(), q.to(DEV).float(), q.to(DEV).float(),
                                        grid, **spec_kw)                    # fp32
+
+
+KERNEL_CASES = [c for c in SMALL if c[2] is None]
+
+
+@pytest.mark.parametrize("name,spec,mode", KERNEL_CASES, ids=[c[0] for c in KERNEL_CASES])
+@pytest.mark.parametrize("kernel", ["single", "grouped"])
+def test_both_kernels_vs_float64_oracle(name, spec, mode, kernel):
+    """The single-window and the grouped kernel each against the oracle, peaky inputs."""
+    n, d = 4, 128
+    g = _geom_of(spec)
+    L = spec.h * spec.w
+    sc = d ** -0.5
+    q = _rand((spec.f_cur * L, n, d), 31, sc * 8).to(DEV)
+    k = _rand((spec.f_kv * L, n, d), 32, sc * 8).to(DEV)
+    v = _rand((spec.f_kv * L, n, d), 33, sc).to(DEV)
+    print(f"[case] {name} kernel={kernel}", flush=True)
+    plan = bgh.build_plan(spec)
+    out = torch.empty_like(q)
+    bgh.run_blockgrid_hip(q, k, v, out, plan=plan, f_cur=spec.f_cur, h=spec.h, w=spec.w, n=n,
+                          d=d, kernel=kernel)
+    torch.cuda.synchronize()
+    ref = obg.window_attention(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                               v.float().cpu().numpy(), g)
+    check_attention(out, ref, label=f"{name}/{kernel}")
+
+
+@pytest.mark.parametrize("cfg", ["c3", "c4"])
+def test_single_kernel_on_benchmark_configs(cfg):
+    """The single-window kernel stays correct on the benchmark sizes the grouped one now runs."""
+    spec = wl.window_spec(cfg)
+    q, k, v, kc, vc = wl.make_window_inputs(cfg, torch.bfloat16, DEV, seed=1, temperature=8.0)
+    q, k, v = q[0].contiguous(), k[0], v[0]
+    if kc is not None:
+        k, v = torch.cat([kc[0], k], 0), torch.cat([vc[0], v], 0)
+    k, v = k.contiguous(), v.contiguous()
+    plan = bgh.build_plan(spec)
+    out = torch.empty_like(q)
+    bgh.run_blockgrid_hip(q, k, v, out, plan=plan, f_cur=spec.f_cur, h=spec.h, w=spec.w,
+                          n=wl.N_HEADS, d=wl.HEAD_DIM, kernel="single")
+    torch.cuda.synchronize()
+    check_attention(out, _gather_ref(spec, None, q, k, v), label=f"{cfg}/single")
+
+
+def test_grouped_kernel_refuses_anchor_plans():
+    spec = att._BlockGridSpec(f_cur=2, f_kv=4, h=8, w=12, block_t=2, bh=4, bw=4, rh=1, rw=1,
+                              rt=1, streaming=True)
+    plan = bgh.build_plan(spec, anchor_mode="chunk")
+    q = torch.zeros(2 * 96, 2, 128, dtype=torch.bfloat16, device=DEV)
+    kv = torch.zeros(2 * 96 + 4 * 96, 2, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="grouped"):
+        bgh.run_blockgrid_hip(q, kv, kv, torch.empty_like(q), plan=plan, f_cur=2, h=8, w=12, n=2,
+                              d=128, anchor_mode="chunk", kernel="grouped")
