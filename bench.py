@@ -40,6 +40,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIG_DESC))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-step", action="store_true",
+                    help="skip the SR-DiT refiner step (30 blocks, hipGraph) measurement")
+    ap.add_argument("--step-iters", type=int, default=5,
+                    help="timed graph replays of the refiner step")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="rough budget for the CPU baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -133,6 +137,72 @@ def cpu_baseline(config, budget_s):
                        f"{med * 1e3:.1f} ms; os.cpu_count()={os.cpu_count()}; {cpu_model}")}
 
 
+def refiner_step(steps, warmup, layers=30):
+    """One SR-DiT 5B refiner step at 2K: 30 blocks + head on 21,600 tokens with 512
+    context tokens, fp8 per-tensor linears, window self-attention as in c3, dense
+    cross-attention, captured once in a HIP graph and replayed."""
+    import torch
+    from sr_dit import model as mdl
+    from sr_dit import workloads as wl
+    from sr_dit.fp8_linear import Fp8Linear
+
+    dev = torch.device("cuda:0")
+    cfg = mdl.SRDiTConfig(num_layers=layers)
+    t0 = time.perf_counter()
+    model = mdl.build_refiner(cfg, device=dev, scaling="tensor", seed=0)
+    build_s = time.perf_counter() - t0
+    f, h, w = 6, 45, 80
+    s_tok = f * h * w
+    geom = model.geometry(f, h, w, cfg.text_len, dev)
+    g = torch.Generator("cpu").manual_seed(0)
+    x = torch.randn(s_tok, cfg.dim, generator=g).to(torch.bfloat16).to(dev)
+    ctx = torch.randn(cfg.text_len, cfg.dim, generator=g).to(torch.bfloat16).to(dev)
+    e0 = (torch.randn(1, 6, cfg.dim, generator=g) / cfg.dim ** 0.5).to(dev)
+    e = (torch.randn(1, cfg.dim, generator=g) / cfg.dim ** 0.5).to(dev)
+
+    def fwd():
+        y = model.blocks_forward(x, e0, ctx, geom)
+        return model.head(y, e)
+
+    # useful work: every fp8 GEMM (2*M*N*K), window attention and cross-attention
+    gemm = 0
+    for blk in model.blocks:
+        for m in blk.modules():
+            if isinstance(m, Fp8Linear):
+                rows = cfg.text_len if m in (blk.cross_attn.k, blk.cross_attn.v) else s_tok
+                gemm += 2 * rows * m.in_features * m.out_features
+    win = wl.plan_useful_flops(geom["plan"]) * layers
+    cross = 4 * s_tok * cfg.text_len * cfg.head_dim * cfg.num_heads * layers
+    total = gemm + win + cross
+    with torch.no_grad():
+        for _ in range(max(1, warmup)):
+            fwd()
+        torch.cuda.synchronize()
+        e0_ev, e1_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0_ev.record()
+        fwd()
+        e1_ev.record()
+        torch.cuda.synchronize()
+        eager_ms = e0_ev.elapsed_time(e1_ev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fwd()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0_ev.record()
+        for _ in range(steps):
+            graph.replay()
+        e1_ev.record()
+        torch.cuda.synchronize()
+        ms = e0_ev.elapsed_time(e1_ev) / steps
+    return {"ms_per_step": round(ms, 3), "eager_ms": round(eager_ms, 3), "steps": steps,
+            "hip_graph": True, "layers": layers, "tokens": s_tok, "context_tokens": cfg.text_len,
+            "linears": "fp8 e4m3, per-tensor scales", "useful_tflop": round(total / 1e12, 2),
+            "gemm_tflop": round(gemm / 1e12, 2), "tflops": round(total / (ms * 1e-3) / 1e12, 1),
+            "build_s": round(build_s, 1),
+            "data": "synthetic: N(0,0.02) weights, N(0,1) activations and context"}
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -208,6 +278,8 @@ def main():
                      "algorithmic_hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1)},
         "wall_s_timed_region": round(wall, 4),
     }
+    if not args.no_step:
+        result["refiner_step"] = refiner_step(args.step_iters, 1)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -1,0 +1,390 @@
+"""SR-DiT 5B refiner block stack on the gfx950 kernels: inference forward.
+
+Restates the pieces of video_refiner/wan/modules/sr_dit/models.py that one
+refiner step runs:
+
+* ``WanRMSNorm`` (models.py:424-440) and ``WanLayerNorm`` (:443-503), fp32;
+* 3-D RoPE: ``rope_params`` (:80-88), ``_rope_axis_dims`` (:91-97) and
+  ``rope_apply`` (:173-214);
+* ``WanSelfAttention.forward``'s window path (:583-676): q/k/v projections,
+  RMSNorm on q and k, RoPE, block-grid window attention, output projection;
+* ``WanT2VCrossAttention.forward`` (:1042-1062): dense attention of every video
+  token over the text context;
+* ``WanAttentionBlock.forward``'s non-teacher-forcing path (:1304-1351) with
+  ``cross_attn_ffn`` (:1256-1262): adaLN modulation, residuals, GELU(tanh) FFN;
+* ``Head`` (:1357-1384), ``sinusoidal_embedding_1d`` (:67-77), the time and
+  text embeddings of ``_prepare_embeddings`` (:1827-1875) and ``unpatchify``
+  (:2234-2257).
+
+Every Linear inside a block is an ``Fp8Linear`` (HIP fp8 GEMM); self-attention
+is the HIP block-grid window kernel; cross-attention runs on the same kernel
+with a plan of 64-token query windows that all see the whole text context.
+Weights are random-initialised (no checkpoint); the module is inference-only.
+
+RoPE is evaluated in fp32 where the reference uses complex128; the rotated
+values are rounded to bf16 either way, and the fp32 rotation differs from the
+fp64 one by ~1e-7 relative before that rounding.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import attention as att
+from . import blockgrid_hip as bgh
+from .fp8_linear import Fp8Linear
+
+
+@dataclass(frozen=True)
+class SRDiTConfig:
+    """Architecture of the 5B refiner (video_refiner/configs/sr_dit_5b.yaml:29-55)."""
+    dim: int = 3072
+    ffn_dim: int = 14336
+    num_heads: int = 24
+    num_layers: int = 30
+    in_dim: int = 48
+    out_dim: int = 48
+    patch_size: tuple = (1, 2, 2)
+    freq_dim: int = 256
+    text_dim: int = 4096
+    text_len: int = 512
+    eps: float = 1e-6
+    rope_theta: float = 10000.0
+    rope_max_seq_len: int = 1024
+    # window geometry of the benchmark: 8x8 blocks, 3x3 neighbourhood, +-1 frame
+    block_hw: tuple = (8, 8)
+    block_radius_hw: tuple = (1, 1)
+    sym_radius_t: int = 1
+
+    @property
+    def head_dim(self) -> int:
+        return self.dim // self.num_heads
+
+
+class RMSNorm(nn.Module):
+    """models.py:424-440: x * rsqrt(mean(x^2) + eps) in fp32, back to x's dtype, * weight."""
+
+    def __init__(self, dim, eps=1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)).type_as(x) * self.weight
+
+
+class LayerNormF32(nn.LayerNorm):
+    """models.py:443-503 (non-DTensor path): layer_norm in fp32, back to x's dtype."""
+
+    def __init__(self, dim, eps=1e-6, elementwise_affine=False):
+        super().__init__(dim, elementwise_affine=elementwise_affine, eps=eps)
+
+    def forward(self, x):
+        w = self.weight.float() if self.weight is not None else None
+        b = self.bias.float() if self.bias is not None else None
+        return F.layer_norm(x.float(), self.normalized_shape, w, b, self.eps).type_as(x)
+
+
+def rope_axis_dims(head_dim: int) -> tuple:
+    """Real RoPE dims along T/H/W (models.py:91-97): 128 -> (44, 42, 42)."""
+    return (head_dim - 4 * (head_dim // 6), 2 * (head_dim // 6), 2 * (head_dim // 6))
+
+
+def rope_params(max_seq_len, dim, theta=10000.0):
+    """models.py:80-88: complex128 [max_seq_len, dim/2] unit phasors pos * theta^(-2i/dim)."""
+    pos = torch.arange(max_seq_len, dtype=torch.float64)
+    inv = 1.0 / torch.pow(theta, torch.arange(0, dim, 2, dtype=torch.float64).div(dim))
+    ang = torch.outer(pos, inv)
+    return torch.polar(torch.ones_like(ang), ang)
+
+
+def rope_table(cfg: SRDiTConfig, f, h, w, t_offset=0, device="cuda"):
+    """Per-token complex64 rotation [f*h*w, 1, head_dim/2] for a (f, h, w) grid.
+
+    The frequency split follows rope_apply (models.py:176-178): c = head_dim/2
+    complex pairs split [c - 2(c//3), c//3, c//3] over (t, h, w).
+    """
+    d = cfg.head_dim
+    dt, dh, dw = rope_axis_dims(d)
+    c = d // 2
+    ft = rope_params(cfg.rope_max_seq_len, dt, cfg.rope_theta)
+    fh = rope_params(cfg.rope_max_seq_len, dh, cfg.rope_theta)
+    fw = rope_params(cfg.rope_max_seq_len, dw, cfg.rope_theta)
+    assert ft.shape[1] + fh.shape[1] + fw.shape[1] == c
+    tab = torch.cat([
+        ft[t_offset:t_offset + f].view(f, 1, 1, -1).expand(f, h, w, -1),
+        fh[:h].view(1, h, 1, -1).expand(f, h, w, -1),
+        fw[:w].view(1, 1, w, -1).expand(f, h, w, -1)], dim=-1).reshape(f * h * w, 1, c)
+    return tab.to(torch.complex64).to(device)
+
+
+def rope_apply(x, table):
+    """x [s, n, d] (bf16) rotated pairwise by table [s, 1, d/2]; result in x's dtype."""
+    s, n, d = x.shape
+    xc = torch.view_as_complex(x.float().reshape(s, n, d // 2, 2))
+    return torch.view_as_real(xc * table).reshape(s, n, d).to(x.dtype)
+
+
+def sinusoidal_embedding_1d(dim, position):
+    """models.py:67-77, float64."""
+    half = dim // 2
+    position = position.to(torch.float64)
+    sinusoid = torch.outer(position, torch.pow(10000, -torch.arange(half).to(position).div(half)))
+    return torch.cat([torch.cos(sinusoid), torch.sin(sinusoid)], dim=1)
+
+
+class CrossAttentionPlan:
+    """Dense attention of Lq video tokens over Lc context tokens on the window kernel.
+
+    The query tokens are laid out as one frame of a 1 x Lq grid; window i holds
+    queries [64i, 64i + 64) and its KV cuboid is columns [0, Lc) of that grid,
+    i.e. context tokens 0 .. Lc-1.  Rows use the plain 19-field layout with no
+    anchor.
+    """
+
+    def __init__(self, lq: int, lc: int):
+        rows = []
+        for q0 in range(0, lq, 64):
+            ql = min(64, lq - q0)
+            rows.append([0, 1, 0, q0, 1, ql, 0, 1, 0, 1, 0, lc, 0, 0, 1, 0, lc, 1, lq])
+        self.lq, self.lc = lq, lc
+        self.plan = {"params": torch.tensor(rows, dtype=torch.int32), "n_w": len(rows),
+                     "block_m": 64, "m_tiles": 1, "block_n": 64, "hr_base": 0,
+                     "p_stride": bgh.P_PLAIN}
+
+    def run(self, q, k, v, out):
+        bgh.run_blockgrid_hip(q, k, v, out, plan=self.plan, f_cur=1, h=1, w=self.lq,
+                              n=q.shape[1], d=q.shape[2])
+        return out
+
+
+class SelfAttention(nn.Module):
+    """WanSelfAttention, window path (models.py:583-676), one sample."""
+
+    def __init__(self, cfg: SRDiTConfig):
+        super().__init__()
+        self.cfg = cfg
+        dim = cfg.dim
+        self.q = nn.Linear(dim, dim)
+        self.k = nn.Linear(dim, dim)
+        self.v = nn.Linear(dim, dim)
+        self.o = nn.Linear(dim, dim)
+        self.norm_q = RMSNorm(dim, eps=cfg.eps)
+        self.norm_k = RMSNorm(dim, eps=cfg.eps)
+
+    def forward(self, x, geom):
+        """x [s, dim] -> [s, dim]; geom: the step's geometry (SRDiT.geometry)."""
+        n, d = self.cfg.num_heads, self.cfg.head_dim
+        s = x.shape[0]
+        q = self.norm_q(self.q(x)).view(s, n, d)
+        k = self.norm_k(self.k(x)).view(s, n, d)
+        v = self.v(x).view(s, n, d)
+        q = rope_apply(q, geom["rope"]).contiguous()
+        k = rope_apply(k, geom["rope"]).contiguous()
+        out = torch.empty_like(q)
+        f, h, w = geom["grid"]
+        bgh.run_blockgrid_hip(q, k, v.contiguous(), out, plan=geom["plan"], f_cur=f, h=h, w=w,
+                              n=n, d=d)
+        return self.o(out.view(s, n * d))
+
+
+class CrossAttention(nn.Module):
+    """WanT2VCrossAttention (models.py:1042-1062), one sample, no context lengths."""
+
+    def __init__(self, cfg: SRDiTConfig):
+        super().__init__()
+        self.cfg = cfg
+        dim = cfg.dim
+        self.q = nn.Linear(dim, dim)
+        self.k = nn.Linear(dim, dim)
+        self.v = nn.Linear(dim, dim)
+        self.o = nn.Linear(dim, dim)
+        self.norm_q = RMSNorm(dim, eps=cfg.eps)
+        self.norm_k = RMSNorm(dim, eps=cfg.eps)
+
+    def forward(self, x, context, geom):
+        n, d = self.cfg.num_heads, self.cfg.head_dim
+        s, lc = x.shape[0], context.shape[0]
+        q = self.norm_q(self.q(x)).view(s, n, d).contiguous()
+        k = self.norm_k(self.k(context)).view(lc, n, d).contiguous()
+        v = self.v(context).view(lc, n, d).contiguous()
+        out = torch.empty_like(q)
+        geom["cross"].run(q, k, v, out)
+        return self.o(out.view(s, n * d))
+
+
+class Block(nn.Module):
+    """WanAttentionBlock, non-teacher-forcing forward (models.py:1304-1351, :1256-1262)."""
+
+    def __init__(self, cfg: SRDiTConfig):
+        super().__init__()
+        dim = cfg.dim
+        self.norm1 = LayerNormF32(dim, cfg.eps)
+        self.self_attn = SelfAttention(cfg)
+        self.norm3 = LayerNormF32(dim, cfg.eps, elementwise_affine=True)
+        self.cross_attn = CrossAttention(cfg)
+        self.norm2 = LayerNormF32(dim, cfg.eps)
+        self.ffn = nn.Sequential(nn.Linear(dim, cfg.ffn_dim), nn.GELU(approximate="tanh"),
+                                 nn.Linear(cfg.ffn_dim, dim))
+        self.modulation = nn.Parameter(torch.randn(1, 6, dim) / dim ** 0.5)
+
+    def forward(self, x, e, context, geom):
+        """x [s, dim] (bf16), e [1, 6, dim] (fp32), context [lc, dim] -> [s, dim]."""
+        dt = x.dtype
+        ep = (self.modulation.float() + e).chunk(6, dim=1)
+        ep = [t.reshape(1, -1) for t in ep]
+        attn_in = self.norm1(x).float() * (1 + ep[1]) + ep[0]
+        y = self.self_attn(attn_in.to(dt), geom)
+        x = (x.float() + y.float() * ep[2]).to(dt)
+        x = x + self.cross_attn(self.norm3(x), context, geom)
+        ffn_in = self.norm2(x).float() * (1 + ep[4]) + ep[3]
+        y = self.ffn(ffn_in.to(dt))
+        return (x.float() + y.float() * ep[5]).to(dt)
+
+
+class Head(nn.Module):
+    """models.py:1357-1384: modulated LayerNorm and the output Linear, in fp32."""
+
+    def __init__(self, cfg: SRDiTConfig):
+        super().__init__()
+        self.cfg = cfg
+        out = math.prod(cfg.patch_size) * cfg.out_dim
+        self.norm = LayerNormF32(cfg.dim, cfg.eps)
+        self.head = nn.Linear(cfg.dim, out)
+        self.modulation = nn.Parameter(torch.randn(1, 2, cfg.dim) / cfg.dim ** 0.5)
+
+    def forward(self, x, e):
+        m = (self.modulation.float() + e.float().unsqueeze(1)).chunk(2, dim=1)
+        xin = self.norm(x).float() * (1 + m[1].reshape(1, -1)) + m[0].reshape(1, -1)
+        return F.linear(xin, self.head.weight.float(), self.head.bias.float())
+
+
+class SRDiT(nn.Module):
+    """The refiner DiT for one sample: embeddings, blocks, head, unpatchify."""
+
+    def __init__(self, cfg: SRDiTConfig):
+        super().__init__()
+        self.cfg = cfg
+        dim = cfg.dim
+        self.patch_embedding = nn.Conv3d(cfg.in_dim, dim, kernel_size=cfg.patch_size,
+                                         stride=cfg.patch_size)
+        self.text_embedding = nn.Sequential(nn.Linear(cfg.text_dim, dim), nn.GELU(approximate="tanh"),
+                                            nn.Linear(dim, dim))
+        self.time_embedding = nn.Sequential(nn.Linear(cfg.freq_dim, dim), nn.SiLU(),
+                                            nn.Linear(dim, dim))
+        self.time_projection = nn.Sequential(nn.SiLU(), nn.Linear(dim, dim * 6))
+        self.blocks = nn.ModuleList([Block(cfg) for _ in range(cfg.num_layers)])
+        self.head = Head(cfg)
+
+    # -- geometry ---------------------------------------------------------
+    def geometry(self, f, h, w, lc, device, t_offset=0):
+        """Plans and tables for a (f, h, w) token grid and lc context tokens.
+
+        Built once per grid and reused by every block and every step: the
+        window plan (block_hw, radius, +-sym_radius_t frames), the
+        cross-attention plan and the RoPE table.
+        """
+        cfg = self.cfg
+        spec = att._BlockGridSpec(f_cur=f, f_kv=f, h=h, w=w, block_t=1,
+                                  bh=cfg.block_hw[0], bw=cfg.block_hw[1],
+                                  rh=cfg.block_radius_hw[0], rw=cfg.block_radius_hw[1],
+                                  sym_rt=cfg.sym_radius_t)
+        return {"grid": (f, h, w), "plan": bgh.cached_plan(spec),
+                "cross": CrossAttentionPlan(f * h * w, lc),
+                "rope": rope_table(cfg, f, h, w, t_offset, device)}
+
+    # -- forward pieces -----------------------------------------------------
+    def time_embed(self, t):
+        """t [1] -> (e [1, dim], e0 [1, 6, dim]), fp32 (models.py:1845-1849)."""
+        e = self.time_embedding(sinusoidal_embedding_1d(self.cfg.freq_dim, t).float())
+        e0 = self.time_projection(e).unflatten(1, (6, self.cfg.dim))
+        return e, e0
+
+    def blocks_forward(self, x, e0, context, geom):
+        """The 30-block stack: x [s, dim] bf16 -> [s, dim]."""
+        for blk in self.blocks:
+            x = blk(x, e0, context, geom)
+        return x
+
+    def forward(self, latent, t, context_raw, geom):
+        """latent [in_dim, f, 2h, 2w] -> [out_dim, f, 2h, 2w] (one sample)."""
+        cfg = self.cfg
+        dt = self.patch_embedding.weight.dtype
+        x = self.patch_embedding(latent.unsqueeze(0).to(dt))
+        f, h, w = x.shape[2:]
+        x = x.flatten(2).transpose(1, 2)[0].contiguous()
+        ctx = context_raw
+        if ctx.shape[0] < cfg.text_len:
+            ctx = torch.cat([ctx, ctx.new_zeros(cfg.text_len - ctx.shape[0], ctx.shape[1])])
+        ctx = self.text_embedding(ctx.to(dt))
+        e, e0 = self.time_embed(t)
+        x = self.blocks_forward(x, e0, ctx, geom)
+        y = self.head(x, e)
+        return unpatchify(y, (f, h, w), cfg.patch_size, cfg.out_dim)
+
+
+def unpatchify(x, grid, patch_size, c):
+    """models.py:2234-2257: [L, c*prod(patch)] -> [c, f*pt, h*ph, w*pw]."""
+    f, h, w = grid
+    pt, ph, pw = patch_size
+    u = x[: f * h * w].view(f, h, w, pt, ph, pw, c)
+    u = u.permute(6, 0, 3, 1, 4, 2, 5)
+    return u.reshape(c, f * pt, h * ph, w * pw)
+
+
+def init_weights(model: SRDiT, std=0.02, seed=0):
+    """Random N(0, std) Linear/Conv weights, zero biases, N(0,1)/sqrt(dim)
+    modulations (the benchmark's synthetic weights; no checkpoint)."""
+    g = torch.Generator(device=next(model.parameters()).device).manual_seed(seed)
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, (nn.Linear, nn.Conv3d)):
+                m.weight.copy_(torch.randn(m.weight.shape, generator=g, device=m.weight.device) * std)
+                if m.bias is not None:
+                    m.bias.zero_()
+        for blk in model.blocks:
+            blk.modulation.copy_(torch.randn(blk.modulation.shape, generator=g,
+                                             device=blk.modulation.device) / model.cfg.dim ** 0.5)
+        model.head.modulation.copy_(torch.randn(model.head.modulation.shape, generator=g,
+                                                device=model.head.modulation.device)
+                                    / model.cfg.dim ** 0.5)
+    return model
+
+
+def build_refiner(cfg: SRDiTConfig, device="cuda", dtype=torch.bfloat16, fp8=True,
+                  scaling="tensor", seed=0, num_layers=None):
+    """Random-initialised refiner on ``device``; with ``fp8`` every block Linear is an
+    Fp8Linear with ``scaling`` ("tensor" or "rowwise").  Blocks are built and
+    converted one at a time, so only one block's bf16 weights are ever resident."""
+    if num_layers is not None:
+        cfg = SRDiTConfig(**{**cfg.__dict__, "num_layers": int(num_layers)})
+    proto = SRDiTConfig(**{**cfg.__dict__, "num_layers": 0})
+    model = SRDiT(proto).to(device=device, dtype=dtype)
+    init_weights(model, seed=seed)
+    model.cfg = cfg
+    blocks = []
+    for i in range(cfg.num_layers):
+        blk = Block(cfg).to(device=device, dtype=dtype)
+        g = torch.Generator(device=device).manual_seed(seed * 1000 + i + 1)
+        with torch.no_grad():
+            for m in blk.modules():
+                if isinstance(m, nn.Linear):
+                    m.weight.copy_(torch.randn(m.weight.shape, generator=g, device=device) * 0.02)
+                    m.bias.zero_()
+            blk.modulation.copy_(torch.randn(blk.modulation.shape, generator=g, device=device)
+                                 / cfg.dim ** 0.5)
+        if fp8:
+            for parent, names in ((blk.self_attn, ("q", "k", "v", "o")),
+                                  (blk.cross_attn, ("q", "k", "v", "o"))):
+                for nm in names:
+                    setattr(parent, nm, Fp8Linear.from_linear(getattr(parent, nm), scaling=scaling))
+            blk.ffn[0] = Fp8Linear.from_linear(blk.ffn[0], scaling=scaling)
+            blk.ffn[2] = Fp8Linear.from_linear(blk.ffn[2], scaling=scaling)
+        blocks.append(blk)
+    model.blocks = nn.ModuleList(blocks)
+    return model.eval()

@@ -1,0 +1,166 @@
+"""The refiner block stack (fp8 linears, window and cross attention on the HIP
+kernels) against a float32 torch restatement of the same computation.
+
+The restatement follows the reference block (models.py:1304-1351, :1256-1262),
+WanSelfAttention's window path (:583-676) with complex128 RoPE (:173-214),
+WanT2VCrossAttention (:1042-1062) and Fp8Linear (fp8_linear.py:282-297): the
+activation is quantised with the reference formula, the product is the fp32
+dequantised matmul, window attention is dense fp32 attention under the
+oracle's block mask.  bf16 roundings sit at the same points as in the
+reference.  Small sizes: two blocks, dim 256, 2 heads of 128, a 3x16x16 grid.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import blockgrid as obg
+from sr_dit import model as mdl
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+F8 = torch.float8_e4m3fn
+
+
+def _ref_linear(lin, x):
+    """Fp8Linear.forward restated: reference quantiser + fp32 dequantised product."""
+    x2 = x.reshape(-1, lin.in_features)
+    if lin.scaling == "rowwise":
+        amax = x2.abs().amax(dim=-1, keepdim=True).float()
+        xs = (amax / 448.0).clamp_min(1e-12)
+        ws = lin.weight_scale.reshape(1, -1)
+    else:
+        xs = (x2.abs().amax().float() / 448.0).clamp_min(1e-12)
+        ws = lin.weight_scale.reshape(1, 1)
+    xq = (x2.float() / xs).clamp(-448, 448).to(F8)
+    out = (xq.float() @ lin.weight_fp8.float().T) * xs * ws
+    if lin.bias is not None:
+        out = out + lin.bias.float()
+    return out.to(torch.bfloat16).reshape(*x.shape[:-1], lin.out_features)
+
+
+def _ref_rope(x, grid, cfg):
+    """rope_apply (models.py:173-214) in complex128."""
+    f, h, w = grid
+    s, n, d = x.shape
+    c = d // 2
+    dt, dh, dw = mdl.rope_axis_dims(d)
+    ft = mdl.rope_params(cfg.rope_max_seq_len, dt, cfg.rope_theta)
+    fh = mdl.rope_params(cfg.rope_max_seq_len, dh, cfg.rope_theta)
+    fw = mdl.rope_params(cfg.rope_max_seq_len, dw, cfg.rope_theta)
+    fr = torch.cat([ft[:f].view(f, 1, 1, -1).expand(f, h, w, -1),
+                    fh[:h].view(1, h, 1, -1).expand(f, h, w, -1),
+                    fw[:w].view(1, 1, w, -1).expand(f, h, w, -1)], dim=-1).reshape(s, 1, c).to(x.device)
+    xc = torch.view_as_complex(x.to(torch.float64).reshape(s, n, c, 2))
+    return torch.view_as_real(xc * fr).flatten(2).to(x.dtype)
+
+
+def _ref_attention(q, k, v, mask=None):
+    """fp32 softmax attention, [s, n, d] layout, P rounded to bf16 before P.V."""
+    qf, kf, vf = (t.float().transpose(0, 1) for t in (q, k, v))
+    sc = (qf @ kf.transpose(1, 2)) * q.shape[-1] ** -0.5
+    if mask is not None:
+        sc = sc.masked_fill(~mask, float("-inf"))
+    p = torch.softmax(sc, dim=-1)
+    return (p.to(torch.bfloat16).float() @ vf).transpose(0, 1).to(torch.bfloat16)
+
+
+def _ref_block(blk, x, e, ctx, grid, mask, cfg):
+    n, d = cfg.num_heads, cfg.head_dim
+    dtp = x.dtype
+    ep = [t.reshape(1, -1) for t in (blk.modulation.float() + e).chunk(6, dim=1)]
+    attn_in = (blk.norm1(x).float() * (1 + ep[1]) + ep[0]).to(dtp)
+    sa = blk.self_attn
+    s = x.shape[0]
+    q = sa.norm_q(_ref_linear(sa.q, attn_in)).view(s, n, d)
+    k = sa.norm_k(_ref_linear(sa.k, attn_in)).view(s, n, d)
+    v = _ref_linear(sa.v, attn_in).view(s, n, d)
+    q, k = _ref_rope(q, grid, cfg), _ref_rope(k, grid, cfg)
+    y = _ref_linear(sa.o, _ref_attention(q, k, v, mask).reshape(s, n * d))
+    x = (x.float() + y.float() * ep[2]).to(dtp)
+    ca = blk.cross_attn
+    xn = blk.norm3(x)
+    lc = ctx.shape[0]
+    cq = ca.norm_q(_ref_linear(ca.q, xn)).view(s, n, d)
+    ck = ca.norm_k(_ref_linear(ca.k, ctx)).view(lc, n, d)
+    cv = _ref_linear(ca.v, ctx).view(lc, n, d)
+    x = x + _ref_linear(ca.o, _ref_attention(cq, ck, cv).reshape(s, n * d))
+    ffn_in = (blk.norm2(x).float() * (1 + ep[4]) + ep[3]).to(dtp)
+    hmid = F.gelu(_ref_linear(blk.ffn[0], ffn_in).float(), approximate="tanh").to(dtp)
+    y = _ref_linear(blk.ffn[2], hmid)
+    return (x.float() + y.float() * ep[5]).to(dtp)
+
+
+SMALL = mdl.SRDiTConfig(dim=256, ffn_dim=512, num_heads=2, num_layers=2, text_len=64)
+
+
+@pytest.mark.parametrize("scaling", ["tensor", "rowwise"])
+def test_block_stack_matches_fp32_restatement(scaling):
+    print(f"[case] block stack scaling={scaling}", flush=True)
+    cfg = SMALL
+    model = mdl.build_refiner(cfg, device=DEV, scaling=scaling, seed=3)
+    f, h, w = 3, 16, 16
+    geom = model.geometry(f, h, w, cfg.text_len, DEV)
+    g = torch.Generator("cpu").manual_seed(0)
+    x = torch.randn(f * h * w, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+    ctx = torch.randn(cfg.text_len, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+    e0 = (torch.randn(1, 6, cfg.dim, generator=g) / cfg.dim ** 0.5).to(DEV)
+    geo = obg.Geometry(f_cur=f, f_kv=f, h=h, w=w, block_t=1, bh=8, bw=8, rh=1, rw=1, sym_rt=1)
+    mask = torch.from_numpy(obg.dense_mask(geo)).to(DEV)
+    with torch.no_grad():
+        out = model.blocks_forward(x, e0, ctx, geom)
+        ref = x
+        for blk in model.blocks:
+            ref = _ref_block(blk, ref, e0, ctx, (f, h, w), mask, cfg)
+    torch.cuda.synchronize()
+    o, r = out.float(), ref.float()
+    err = (o - r).abs()
+    scale = r.abs().mean().item()
+    print(f"[metrics] max {err.max().item():.3e} mean {err.mean().item():.3e} |ref| {scale:.3e}",
+          flush=True)
+    assert torch.isfinite(o).all()
+    assert err.mean().item() <= 2e-3 * max(1.0, scale)
+    assert err.max().item() <= 5e-2 * max(1.0, r.abs().max().item())
+
+
+def test_rope_fp32_matches_complex128():
+    cfg = mdl.SRDiTConfig()
+    f, h, w = 3, 9, 10
+    x = torch.randn(f * h * w, 24, 128, generator=torch.Generator("cpu").manual_seed(1)).to(
+        torch.bfloat16).to(DEV)
+    ours = mdl.rope_apply(x, mdl.rope_table(cfg, f, h, w, 0, DEV))
+    ref = _ref_rope(x, (f, h, w), cfg)
+    diff = (ours.float() - ref.float()).abs()
+    # equal after the bf16 rounding except where the fp64 product sits on a rounding
+    # boundary; such elements differ by one bf16 step
+    assert (diff > 0).float().mean().item() < 1e-3
+    assert diff.max().item() <= 2 ** -7 * ref.float().abs().max().item()
+
+
+def test_full_size_step_in_a_graph():
+    """30 blocks at the 2K grid (fp8 per-tensor), captured once and replayed: finite,
+    and every replay equals the eager forward on new inputs."""
+    cfg = mdl.SRDiTConfig()
+    print("[case] full-size refiner step graph", flush=True)
+    model = mdl.build_refiner(cfg, device=DEV, scaling="tensor", seed=0, num_layers=4)
+    f, h, w = 6, 45, 80
+    geom = model.geometry(f, h, w, cfg.text_len, DEV)
+    g = torch.Generator("cpu").manual_seed(0)
+    x = torch.randn(f * h * w, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+    ctx = torch.randn(cfg.text_len, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+    e0 = (torch.randn(1, 6, cfg.dim, generator=g) / cfg.dim ** 0.5).to(DEV)
+    with torch.no_grad():
+        model.blocks_forward(x, e0, ctx, geom)         # plans, workspaces, device tables
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y = model.blocks_forward(x, e0, ctx, geom)
+        for it in range(3):
+            x.copy_(torch.randn(x.shape, generator=g).to(torch.bfloat16).to(DEV))
+            graph.replay()
+            torch.cuda.synchronize()
+            want = model.blocks_forward(x, e0, ctx, geom)
+            torch.cuda.synchronize()
+            assert torch.isfinite(y.float()).all()
+            assert torch.equal(y, want), it
