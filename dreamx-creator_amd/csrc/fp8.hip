@@ -196,6 +196,7 @@ struct GemmArgs {
   int64_t ldo;
   int sa_per_row, sb_per_col;
   int tiles_m, tiles_n;
+  uint32_t* amax_out;  // AMAX epilogue only
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -206,6 +207,20 @@ __device__ __forceinline__ i32x8_t read_frag(const uint8_t* lds, int off_lo, int
   return i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// GELU with the tanh approximation, as torch evaluates it in fp32:
+// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
+  const float kKappa = 0.044715f;
+  const float x3 = x * x * x;
+  const float inner = kBeta * (x + kKappa * x3);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// EPI 0: out = bf16(v); EPI 1: out = bf16(gelu(bf16(v))), the Linear's bf16
+// output fed to nn.GELU(approximate='tanh').  AMAX: also the max |out| (float
+// bits) of the whole output into *g.amax_out, for a per-tensor quantiser.
+template <int EPI, bool AMAX>
 __global__ __launch_bounds__(256) void fp8_gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G_STAGE_BYTES];
 
@@ -304,6 +319,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const GemmArgs g) {
   // lane l holds row m = .. + (l & 31) and columns n = .. + 8*(r/4) + 4*(l/32) + r%4.
   const int mrow = lane & 31;
   const int ncol = 4 * (lane >> 5);
+  uint32_t amax = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int m = m0 + wm * 128 + j * 32 + mrow;
@@ -337,14 +353,30 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const GemmArgs g) {
         for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * q + r] * sa * sb[r] + bias[r];
         typedef float f32x2v __attribute__((ext_vector_type(2)));
         typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-        const bf16x2v p0 = __builtin_convertvector(f32x2v{v[0], v[1]}, bf16x2v);
-        const bf16x2v p1 = __builtin_convertvector(f32x2v{v[2], v[3]}, bf16x2v);
+        bf16x2v p0 = __builtin_convertvector(f32x2v{v[0], v[1]}, bf16x2v);
+        bf16x2v p1 = __builtin_convertvector(f32x2v{v[2], v[3]}, bf16x2v);
+        if (EPI == 1) {
+          const uint32_t b0 = __builtin_bit_cast(uint32_t, p0), b1 = __builtin_bit_cast(uint32_t, p1);
+          const float r0 = __uint_as_float(b0 << 16), r1 = __uint_as_float(b0 & 0xffff0000u);
+          const float r2 = __uint_as_float(b1 << 16), r3 = __uint_as_float(b1 & 0xffff0000u);
+          p0 = __builtin_convertvector(f32x2v{gelu_tanh(r0), gelu_tanh(r1)}, bf16x2v);
+          p1 = __builtin_convertvector(f32x2v{gelu_tanh(r2), gelu_tanh(r3)}, bf16x2v);
+        }
         uint2 packed;
         packed.x = __builtin_bit_cast(uint32_t, p0);
         packed.y = __builtin_bit_cast(uint32_t, p1);
+        if (AMAX) {
+          amax = max(amax, max((packed.x & 0x7fffu) << 16, packed.x & 0x7fff0000u));
+          amax = max(amax, max((packed.y & 0x7fffu) << 16, packed.y & 0x7fff0000u));
+        }
         *reinterpret_cast<uint2*>(orow + n) = packed;
       }
     }
+  }
+  if (AMAX) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, o));
+    if (lane == 0) atomicMax(g.amax_out, amax);
   }
 }
 
@@ -412,25 +444,29 @@ extern "C" int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64
   });
 }
 
-extern "C" int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_rows,
-                              const float* sb, int64_t sb_cols, const void* bias, void* out,
-                              int64_t M, int64_t N, int64_t K, int64_t ldo, void* stream) {
-  SRDIT_REQUIRE(a && b && sa && sb && out, "srdit_fp8_gemm: null pointer");
-  SRDIT_REQUIRE(M > 0 && N > 0 && K > 0, "srdit_fp8_gemm: M, N, K must be positive");
-  SRDIT_REQUIRE(K % 128 == 0, "srdit_fp8_gemm: K=%lld must be a multiple of 128", (long long)K);
-  SRDIT_REQUIRE(N % 16 == 0, "srdit_fp8_gemm: N=%lld must be a multiple of 16", (long long)N);
-  SRDIT_REQUIRE(ldo >= N && ldo % 4 == 0, "srdit_fp8_gemm: ldo=%lld must be >= N and a multiple of 4",
+namespace srdit {
+namespace {
+int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_rows, const float* sb,
+                    int64_t sb_cols, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
+                    int64_t ldo, int epilogue, uint32_t* amax_out, void* stream, const char* who) {
+  SRDIT_REQUIRE(a && b && sa && sb && out, "%s: null pointer", who);
+  SRDIT_REQUIRE(M > 0 && N > 0 && K > 0, "%s: M, N, K must be positive", who);
+  SRDIT_REQUIRE(K % 128 == 0, "%s: K=%lld must be a multiple of 128", who, (long long)K);
+  SRDIT_REQUIRE(N % 16 == 0, "%s: N=%lld must be a multiple of 16", who, (long long)N);
+  SRDIT_REQUIRE(ldo >= N && ldo % 4 == 0, "%s: ldo=%lld must be >= N and a multiple of 4", who,
                 (long long)ldo);
   SRDIT_REQUIRE(M * K < (int64_t(1) << 31) && N * K < (int64_t(1) << 31),
-                "srdit_fp8_gemm: M*K and N*K must be below 2^31 (M=%lld N=%lld K=%lld)",
-                (long long)M, (long long)N, (long long)K);
-  SRDIT_REQUIRE(sa_rows == 1 || sa_rows == M, "srdit_fp8_gemm: sa_rows=%lld must be 1 or M",
+                "%s: M*K and N*K must be below 2^31 (M=%lld N=%lld K=%lld)", who, (long long)M,
+                (long long)N, (long long)K);
+  SRDIT_REQUIRE(sa_rows == 1 || sa_rows == M, "%s: sa_rows=%lld must be 1 or M", who,
                 (long long)sa_rows);
-  SRDIT_REQUIRE(sb_cols == 1 || sb_cols == N, "srdit_fp8_gemm: sb_cols=%lld must be 1 or N",
+  SRDIT_REQUIRE(sb_cols == 1 || sb_cols == N, "%s: sb_cols=%lld must be 1 or N", who,
                 (long long)sb_cols);
   SRDIT_REQUIRE(aligned16(a) && aligned16(b) && aligned16(sb) && aligned16(out) &&
                     (!bias || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0),
-                "srdit_fp8_gemm: a, b, sb, out must be 16-byte aligned and bias 8-byte aligned");
+                "%s: a, b, sb, out must be 16-byte aligned and bias 8-byte aligned", who);
+  SRDIT_REQUIRE(epilogue == 0 || epilogue == 1, "%s: epilogue %d is not 0 (none) or 1 (gelu)", who,
+                epilogue);
   GemmArgs g;
   g.a = static_cast<const uint8_t*>(a);
   g.b = static_cast<const uint8_t*>(b);
@@ -446,9 +482,52 @@ extern "C" int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int
   g.sb_per_col = sb_cols == N && N > 1;
   g.tiles_m = (int)((M + GT - 1) / GT);
   g.tiles_n = (int)((N + GT - 1) / GT);
+  g.amax_out = amax_out;
   const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
-  SRDIT_REQUIRE(tiles < (int64_t(1) << 31), "srdit_fp8_gemm: too many tiles");
-  fp8_gemm_kernel<<<(unsigned)tiles, 256, 0, static_cast<hipStream_t>(stream)>>>(g);
+  SRDIT_REQUIRE(tiles < (int64_t(1) << 31), "%s: too many tiles", who);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (amax_out) {
+    clear_u32_kernel<<<1, 1, 0, s>>>(amax_out);
+    SRDIT_LAUNCH_CHECK("clear_u32_kernel");
+  }
+  const unsigned grid = (unsigned)tiles;
+  if (epilogue == 0 && !amax_out) fp8_gemm_kernel<0, false><<<grid, 256, 0, s>>>(g);
+  else if (epilogue == 0) fp8_gemm_kernel<0, true><<<grid, 256, 0, s>>>(g);
+  else if (!amax_out) fp8_gemm_kernel<1, false><<<grid, 256, 0, s>>>(g);
+  else fp8_gemm_kernel<1, true><<<grid, 256, 0, s>>>(g);
   SRDIT_LAUNCH_CHECK("fp8_gemm_kernel");
   return SRDIT_OK;
+}
+}  // namespace
+}  // namespace srdit
+
+extern "C" int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_rows,
+                              const float* sb, int64_t sb_cols, const void* bias, void* out,
+                              int64_t M, int64_t N, int64_t K, int64_t ldo, void* stream) {
+  return fp8_gemm_launch(a, b, sa, sa_rows, sb, sb_cols, bias, out, M, N, K, ldo, 0, nullptr,
+                         stream, "srdit_fp8_gemm");
+}
+
+extern "C" int srdit_fp8_gemm_ex(const void* a, const void* b, const float* sa, int64_t sa_rows,
+                                 const float* sb, int64_t sb_cols, const void* bias, void* out,
+                                 int64_t M, int64_t N, int64_t K, int64_t ldo, int epilogue,
+                                 uint32_t* amax_out, void* stream) {
+  return fp8_gemm_launch(a, b, sa, sa_rows, sb, sb_cols, bias, out, M, N, K, ldo, epilogue,
+                         amax_out, stream, "srdit_fp8_gemm_ex");
+}
+
+extern "C" int srdit_fp8_quant_apply(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype,
+                                     void* xq, float* scale, const uint32_t* amax_ws, void* stream) {
+  if (int rc = check_quant_args("srdit_fp8_quant_apply", x, M, K, ldx, xq, scale)) return rc;
+  SRDIT_REQUIRE(amax_ws, "srdit_fp8_quant_apply: null amax word");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dispatch_quant_dtype(dtype, [&](auto tag) -> int {
+    using T = std::remove_const_t<std::remove_pointer_t<decltype(tag)>>;
+    const int64_t rows4 = (M + 3) / 4;
+    const unsigned blocks = (unsigned)(rows4 < 4096 ? rows4 : 4096);
+    quant_tensor_kernel<T><<<blocks, 256, 0, s>>>(static_cast<const T*>(x), M, K, ldx,
+                                                  static_cast<uint8_t*>(xq), scale, amax_ws);
+    SRDIT_LAUNCH_CHECK("quant_tensor_kernel");
+    return SRDIT_OK;
+  });
 }

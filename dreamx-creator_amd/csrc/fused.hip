@@ -1,0 +1,294 @@
+// Fused row kernels of the refiner block for gfx950: one pass over HBM each.
+//
+//   ln_modulate    out = bf16( f32(bf16(LayerNorm(x) [* w + b])) * (1 + scale) + shift )
+//                  and, optionally, the max |out| (float bits) into an amax word
+//                  for a per-tensor fp8 quantiser of `out`
+//   residual_gate  out = bf16( f32(x) + f32(y) * gate )
+//   rmsnorm_rope   out = RoPE( bf16( f32(bf16(x * rsqrt(mean(x^2) + eps))) * f32(w) ) )
+//
+// They restate, op for op, the elementwise chains of the reference block
+// (video_refiner/wan/modules/sr_dit/models.py): WanLayerNorm (:443-503) and the
+// adaLN modulation of WanAttentionBlock.forward (:1308, :1258); the gated
+// residuals (:1344, :1260); WanRMSNorm (:424-440) on q and k followed by
+// rope_apply (:173-214).  Each fp32 operation rounds where torch's separate
+// kernels round: this file is compiled with -ffp-contract=off, so no multiply
+// and add are contracted into an fma.  The reductions (mean, variance, mean of
+// squares) sum in a different order than torch's.
+//
+// One wavefront per row; a row is read from HBM once (later passes over it hit
+// L1/L2).  K % 8 == 0, rows 16-byte aligned.
+#include "common.h"
+
+namespace srdit {
+namespace {
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4 v, float f[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+// Round to bf16 (nearest even) and back: the value torch holds after .to(bf16).
+__device__ __forceinline__ float bf16_round(float x) {
+  const bf16x2v b = __builtin_convertvector(f32x2v{x, 0.f}, bf16x2v);
+  return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint32_t, b) & 0xffffu) << 16);
+}
+
+__device__ __forceinline__ uint4 pack_bf16x8(const float f[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{f[2 * i], f[2 * i + 1]}, bf16x2v));
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
+  return v;
+}
+
+__global__ void clear_word_kernel(uint32_t* p) { *p = 0u; }
+
+// LayerNorm over each row of x [M, K] (bf16, row stride ldx), eps, optional
+// affine (w, b bf16 [K]); then, with MOD, the adaLN modulation (scale, shift
+// fp32 [K]).  Output bf16 [M, K] with row stride ldo.
+template <bool AFFINE, bool MOD, bool AMAX>
+__global__ __launch_bounds__(256) void ln_modulate_kernel(
+    const uint16_t* __restrict__ x, int64_t M, int K, int64_t ldx, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ b, const float* __restrict__ scale, const float* __restrict__ shift,
+    float eps, uint16_t* __restrict__ out, int64_t ldo, uint32_t* __restrict__ amax_ws) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+  const int nc = K >> 3;
+  float s = 0.f;
+  for (int c = lane; c < nc; c += 64) {
+    float f[8];
+    unpack_bf16x8(xr[c], f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += f[i];
+  }
+  const float mean = wave_sum(s) / static_cast<float>(K);
+  float v = 0.f;
+  for (int c = lane; c < nc; c += 64) {
+    float f[8];
+    unpack_bf16x8(xr[c], f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float d = f[i] - mean;
+      v += d * d;
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(v) / static_cast<float>(K) + eps);
+  uint4* orow = reinterpret_cast<uint4*>(out + row * ldo);
+  uint32_t am = 0;
+  for (int c = lane; c < nc; c += 64) {
+    float f[8];
+    unpack_bf16x8(xr[c], f);
+    float wv[8], bv[8];
+    if (AFFINE) {
+      unpack_bf16x8(reinterpret_cast<const uint4*>(w)[c], wv);
+      unpack_bf16x8(reinterpret_cast<const uint4*>(b)[c], bv);
+    }
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float y = __fmul_rn(f[i] - mean, rstd);
+      if (AFFINE) y = __fadd_rn(__fmul_rn(y, wv[i]), bv[i]);
+      y = bf16_round(y);  // LayerNorm(...).type_as(x)
+      if (MOD) {
+        const int k = 8 * c + i;
+        y = __fadd_rn(__fmul_rn(y, __fadd_rn(1.0f, scale[k])), shift[k]);
+      }
+      o[i] = y;
+    }
+    const uint4 pk = pack_bf16x8(o);
+    orow[c] = pk;
+    if (AMAX) {
+      const uint32_t ww[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        am = max(am, max((ww[i] & 0x7fffu) << 16, (ww[i] & 0x7fff0000u)));
+    }
+  }
+  if (AMAX) {
+    am = wave_umax(am);
+    if (lane == 0) atomicMax(amax_ws, am);
+  }
+}
+
+// out = bf16(f32(x) + f32(y) * gate[k]); out may alias x.
+__global__ __launch_bounds__(256) void residual_gate_kernel(const uint16_t* x, int64_t M, int K,
+                                                            int64_t ldx, const uint16_t* __restrict__ y,
+                                                            int64_t ldy, const float* __restrict__ gate,
+                                                            uint16_t* out, int64_t ldo) {
+  const int nc = K >> 3;
+  const int64_t total = M * nc;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t row = idx / nc;
+    const int c = static_cast<int>(idx - row * nc);
+    float xf[8], yf[8], o[8];
+    unpack_bf16x8(reinterpret_cast<const uint4*>(x + row * ldx)[c], xf);
+    unpack_bf16x8(reinterpret_cast<const uint4*>(y + row * ldy)[c], yf);
+    const float4 g0 = reinterpret_cast<const float4*>(gate)[2 * c];
+    const float4 g1 = reinterpret_cast<const float4*>(gate)[2 * c + 1];
+    const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = __fadd_rn(xf[i], __fmul_rn(yf[i], g[i]));
+    reinterpret_cast<uint4*>(out + row * ldo)[c] = pack_bf16x8(o);
+  }
+}
+
+// RMSNorm over the whole row (K = heads * head_dim), weight w (bf16 [K]), then
+// (ROPE) RoPE on each head: pair j of a head rotated by (cos, sin) = cs[row][j % (head_dim/2)].
+template <bool ROPE>
+__global__ __launch_bounds__(256) void rmsnorm_rope_kernel(const uint16_t* __restrict__ x, int64_t M,
+                                                           int K, int64_t ldx,
+                                                           const uint16_t* __restrict__ w, float eps,
+                                                           const float2* __restrict__ cs, int half_d,
+                                                           uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+  const int nc = K >> 3;
+  float ss = 0.f;
+  for (int c = lane; c < nc; c += 64) {
+    float f[8];
+    unpack_bf16x8(xr[c], f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += __fmul_rn(f[i], f[i]);
+  }
+  const float r = rsqrtf(__fadd_rn(wave_sum(ss) / static_cast<float>(K), eps));
+  const float2* csr = cs + row * half_d;
+  uint4* orow = reinterpret_cast<uint4*>(out + row * K);
+  for (int c = lane; c < nc; c += 64) {
+    float f[8], wv[8], o[8];
+    unpack_bf16x8(xr[c], f);
+    unpack_bf16x8(reinterpret_cast<const uint4*>(w)[c], wv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = bf16_round(__fmul_rn(bf16_round(__fmul_rn(f[i], r)), wv[i]));
+    if (ROPE) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int j = ((8 * c) >> 1) + p;  // pair index within the row
+        const float2 t = csr[j % half_d];
+        const float a = f[2 * p], bb = f[2 * p + 1];
+        o[2 * p] = __fsub_rn(__fmul_rn(a, t.x), __fmul_rn(bb, t.y));
+        o[2 * p + 1] = __fadd_rn(__fmul_rn(a, t.y), __fmul_rn(bb, t.x));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = f[i];
+    }
+    orow[c] = pack_bf16x8(o);
+  }
+}
+
+int check_rows(const char* who, const void* x, int64_t M, int K, int64_t ldx, const void* out,
+               int64_t ldo) {
+  SRDIT_REQUIRE(x && out, "%s: null pointer", who);
+  SRDIT_REQUIRE(M > 0 && K > 0 && K % 8 == 0 && K <= (1 << 20),
+                "%s: M=%lld K=%d (K must be a positive multiple of 8)", who, (long long)M, K);
+  SRDIT_REQUIRE(ldx >= K && ldx % 8 == 0 && ldo >= K && ldo % 8 == 0,
+                "%s: row strides ldx=%lld ldo=%lld must be >= K and multiples of 8", who,
+                (long long)ldx, (long long)ldo);
+  SRDIT_REQUIRE(aligned16(x) && aligned16(out), "%s: x and out must be 16-byte aligned", who);
+  return SRDIT_OK;
+}
+
+}  // namespace
+}  // namespace srdit
+
+using namespace srdit;
+
+extern "C" int srdit_ln_modulate(const void* x, int64_t M, int K, int64_t ldx, const void* ln_w,
+                                 const void* ln_b, const float* scale, const float* shift, float eps,
+                                 void* out, int64_t ldo, uint32_t* amax_ws, void* stream) {
+  if (int rc = check_rows("srdit_ln_modulate", x, M, K, ldx, out, ldo)) return rc;
+  SRDIT_REQUIRE((ln_w == nullptr) == (ln_b == nullptr),
+                "srdit_ln_modulate: give both affine tensors or neither");
+  SRDIT_REQUIRE((scale == nullptr) == (shift == nullptr),
+                "srdit_ln_modulate: give both modulation tensors or neither");
+  SRDIT_REQUIRE((!ln_w || (aligned16(ln_w) && aligned16(ln_b))) &&
+                    (!scale || ((reinterpret_cast<uintptr_t>(scale) & 3) == 0 &&
+                                (reinterpret_cast<uintptr_t>(shift) & 3) == 0)),
+                "srdit_ln_modulate: misaligned affine or modulation tensor");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (amax_ws) {
+    clear_word_kernel<<<1, 1, 0, s>>>(amax_ws);
+    SRDIT_LAUNCH_CHECK("clear_word_kernel");
+  }
+  const unsigned blocks = static_cast<unsigned>((M + 3) / 4);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* wp = static_cast<const uint16_t*>(ln_w);
+  const uint16_t* bp = static_cast<const uint16_t*>(ln_b);
+  uint16_t* op = static_cast<uint16_t*>(out);
+#define SRDIT_LN_LAUNCH(A, MO, AM)                                                              \
+  ln_modulate_kernel<A, MO, AM><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, bp, scale, shift, eps, \
+                                                       op, ldo, amax_ws)
+  const bool af = ln_w != nullptr, mo = scale != nullptr, am = amax_ws != nullptr;
+  if (af && mo && am) SRDIT_LN_LAUNCH(true, true, true);
+  else if (af && mo) SRDIT_LN_LAUNCH(true, true, false);
+  else if (af && am) SRDIT_LN_LAUNCH(true, false, true);
+  else if (af) SRDIT_LN_LAUNCH(true, false, false);
+  else if (mo && am) SRDIT_LN_LAUNCH(false, true, true);
+  else if (mo) SRDIT_LN_LAUNCH(false, true, false);
+  else if (am) SRDIT_LN_LAUNCH(false, false, true);
+  else SRDIT_LN_LAUNCH(false, false, false);
+#undef SRDIT_LN_LAUNCH
+  SRDIT_LAUNCH_CHECK("ln_modulate_kernel");
+  return SRDIT_OK;
+}
+
+extern "C" int srdit_residual_gate(const void* x, const void* y, const float* gate, int64_t M, int K,
+                                   int64_t ldx, int64_t ldy, void* out, int64_t ldo, void* stream) {
+  if (int rc = check_rows("srdit_residual_gate", x, M, K, ldx, out, ldo)) return rc;
+  SRDIT_REQUIRE(y && gate && aligned16(y) && aligned16(gate) && ldy >= K && ldy % 8 == 0,
+                "srdit_residual_gate: y / gate missing or misaligned, or bad ldy");
+  const int64_t total = M * (K / 8);
+  const int64_t want = (total + 255) / 256;
+  const unsigned blocks = static_cast<unsigned>(want < 65536 ? want : 65536);
+  residual_gate_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(x), M, K, ldx, static_cast<const uint16_t*>(y), ldy, gate,
+      static_cast<uint16_t*>(out), ldo);
+  SRDIT_LAUNCH_CHECK("residual_gate_kernel");
+  return SRDIT_OK;
+}
+
+extern "C" int srdit_rmsnorm_rope(const void* x, int64_t M, int K, int64_t ldx, const void* w,
+                                  float eps, const float* rope_cs, int head_dim, void* out,
+                                  void* stream) {
+  if (int rc = check_rows("srdit_rmsnorm_rope", x, M, K, ldx, out, K)) return rc;
+  SRDIT_REQUIRE(w && aligned16(w) && (reinterpret_cast<uintptr_t>(rope_cs) & 7) == 0,
+                "srdit_rmsnorm_rope: weight missing or weight / rope table misaligned");
+  SRDIT_REQUIRE(head_dim > 0 && head_dim % 8 == 0 && K % head_dim == 0,
+                "srdit_rmsnorm_rope: head_dim %d must be a multiple of 8 dividing K=%d", head_dim, K);
+  const unsigned blocks = static_cast<unsigned>((M + 3) / 4);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rope_cs)
+    rmsnorm_rope_kernel<true><<<blocks, 256, 0, s>>>(
+        static_cast<const uint16_t*>(x), M, K, ldx, static_cast<const uint16_t*>(w), eps,
+        reinterpret_cast<const float2*>(rope_cs), head_dim / 2, static_cast<uint16_t*>(out));
+  else
+    rmsnorm_rope_kernel<false><<<blocks, 256, 0, s>>>(
+        static_cast<const uint16_t*>(x), M, K, ldx, static_cast<const uint16_t*>(w), eps, nullptr,
+        head_dim / 2, static_cast<uint16_t*>(out));
+  SRDIT_LAUNCH_CHECK("rmsnorm_rope_kernel");
+  return SRDIT_OK;
+}

@@ -33,6 +33,16 @@ SIGNATURES = {
                                         _c_p]),
     "srdit_fp8_gemm": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p,
                                 _c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
+    "srdit_fp8_gemm_ex": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p,
+                                   _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p]),
+    "srdit_fp8_quant_apply": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
+                                       _c_p]),
+    "srdit_ln_modulate": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_f,
+                                   _c_p, _c_i64, _c_p, _c_p]),
+    "srdit_residual_gate": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_int, _c_i64, _c_i64, _c_p,
+                                     _c_i64, _c_p]),
+    "srdit_rmsnorm_rope": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_f, _c_p, _c_int, _c_p,
+                                    _c_p]),
     "srdit_last_error": (_c_int, [ctypes.c_char_p, _c_int]),
     "srdit_version": (_c_int, []),
     "srdit_copy_bytes": (_c_int, [_c_p, _c_p, _c_i64, _c_p]),
@@ -158,6 +168,57 @@ def fp8_gemm(a, b, sa, sb, bias, out):
                                int(sb.numel()), _ptr(bias), _ptr(out), M, N, K,
                                out.stride(0), _stream(a.device))
     _check(rc, "srdit_fp8_gemm")
+
+
+def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None):
+    """fp8_gemm with an epilogue (0 none, 1 GELU-tanh) and an optional amax word."""
+    M, K = a.shape
+    N = b.shape[0]
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError(f"fp8_gemm_ex: out must be bf16 [{M}, {N}] with unit column stride")
+    rc = load().srdit_fp8_gemm_ex(_ptr(a), _ptr(b), _ptr(sa), int(sa.numel()), _ptr(sb),
+                                  int(sb.numel()), _ptr(bias), _ptr(out), M, N, K, out.stride(0),
+                                  int(epilogue), _ptr(amax_out), _stream(a.device))
+    _check(rc, "srdit_fp8_gemm_ex")
+
+
+def fp8_quant_apply(x, xq, scale, amax_ws):
+    M, K, ldx, dt = _quant_args(x, xq)
+    rc = load().srdit_fp8_quant_apply(_ptr(x), M, K, ldx, dt, _ptr(xq), _ptr(scale), _ptr(amax_ws),
+                                      _stream(x.device))
+    _check(rc, "srdit_fp8_quant_apply")
+
+
+def _bf16_rows(name, t):
+    if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D bf16 tensor with unit column stride")
+
+
+def ln_modulate(x, ln_w, ln_b, scale, shift, eps, out, amax_ws=None):
+    _bf16_rows("ln_modulate x", x)
+    _bf16_rows("ln_modulate out", out)
+    M, K = x.shape
+    rc = load().srdit_ln_modulate(_ptr(x), M, K, x.stride(0), _ptr(ln_w), _ptr(ln_b), _ptr(scale),
+                                  _ptr(shift), float(eps), _ptr(out), out.stride(0), _ptr(amax_ws),
+                                  _stream(x.device))
+    _check(rc, "srdit_ln_modulate")
+
+
+def residual_gate(x, y, gate, out):
+    for nm, t in (("x", x), ("y", y), ("out", out)):
+        _bf16_rows(f"residual_gate {nm}", t)
+    M, K = x.shape
+    rc = load().srdit_residual_gate(_ptr(x), _ptr(y), _ptr(gate), M, K, x.stride(0), y.stride(0),
+                                    _ptr(out), out.stride(0), _stream(x.device))
+    _check(rc, "srdit_residual_gate")
+
+
+def rmsnorm_rope(x, w, eps, rope_cs, head_dim, out):
+    _bf16_rows("rmsnorm_rope x", x)
+    M, K = x.shape
+    rc = load().srdit_rmsnorm_rope(_ptr(x), M, K, x.stride(0), _ptr(w), float(eps), _ptr(rope_cs),
+                                   int(head_dim), _ptr(out), _stream(x.device))
+    _check(rc, "srdit_rmsnorm_rope")
 
 
 def copy_bytes(src, dst, nbytes):

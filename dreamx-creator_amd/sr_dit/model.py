@@ -34,9 +34,10 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _lib
 from . import attention as att
 from . import blockgrid_hip as bgh
-from .fp8_linear import Fp8Linear
+from .fp8_linear import FP8_DTYPE, Fp8Linear, quantize_tensor
 
 
 @dataclass(frozen=True)
@@ -233,8 +234,17 @@ class Block(nn.Module):
                                  nn.Linear(cfg.ffn_dim, dim))
         self.modulation = nn.Parameter(torch.randn(1, 6, dim) / dim ** 0.5)
 
+    def fusable(self) -> bool:
+        """All Linears are per-tensor Fp8Linear: the fused forward applies."""
+        lins = (self.self_attn.q, self.self_attn.k, self.self_attn.v, self.self_attn.o,
+                self.cross_attn.q, self.cross_attn.k, self.cross_attn.v, self.cross_attn.o,
+                self.ffn[0], self.ffn[2])
+        return all(isinstance(m, Fp8Linear) and m.scaling == "tensor" for m in lins)
+
     def forward(self, x, e, context, geom):
         """x [s, dim] (bf16), e [1, 6, dim] (fp32), context [lc, dim] -> [s, dim]."""
+        if FUSED and x.dtype == torch.bfloat16 and self.fusable():
+            return self.forward_fused(x, e, context, geom)
         dt = x.dtype
         ep = (self.modulation.float() + e).chunk(6, dim=1)
         ep = [t.reshape(1, -1) for t in ep]
@@ -245,6 +255,82 @@ class Block(nn.Module):
         ffn_in = self.norm2(x).float() * (1 + ep[4]) + ep[3]
         y = self.ffn(ffn_in.to(dt))
         return (x.float() + y.float() * ep[5]).to(dt)
+
+
+    def forward_fused(self, x, e, context, geom):
+        """The same block with the elementwise chains fused into single-pass kernels.
+
+        LayerNorm + modulation (+ the amax of its output), RMSNorm + RoPE and
+        the gated residuals are one kernel each; the per-tensor fp8 quantiser
+        of a Linear's input reuses the amax its producer wrote, and one
+        quantised input feeds q, k and v (likewise the text context for the
+        cross-attention k and v); the FFN's GELU and the amax of its output run
+        in the first FFN GEMM's epilogue.  The arithmetic at each point is the
+        reference's (models.py:1304-1351); only reduction orders differ.
+        """
+        sa, ca = self.self_attn, self.cross_attn
+        cfg = sa.cfg
+        s, dim = x.shape
+        n, d = cfg.num_heads, cfg.head_dim
+        dev, bf = x.device, torch.bfloat16
+        f, h, w = geom["grid"]
+        amax = geom["amax"]
+        a0, a1 = amax[0:1], amax[1:2]
+        mod = (self.modulation.float() + e).reshape(6, dim).contiguous()
+
+        def quant_from(t, word):
+            tq = torch.empty(t.shape, dtype=FP8_DTYPE, device=dev)
+            ts = torch.empty(1, dtype=torch.float32, device=dev)
+            _lib.fp8_quant_apply(t, tq, ts, word)
+            return tq, ts
+
+        # self-attention
+        attn_in = torch.empty(s, dim, dtype=bf, device=dev)
+        _lib.ln_modulate(x, None, None, mod[1], mod[0], self.norm1.eps, attn_in, a0)
+        xq, xs = quant_from(attn_in, a0)
+        q_lin, k_lin, v = sa.q.gemm(xq, xs), sa.k.gemm(xq, xs), sa.v.gemm(xq, xs)
+        q = torch.empty(s, dim, dtype=bf, device=dev)
+        k = torch.empty(s, dim, dtype=bf, device=dev)
+        _lib.rmsnorm_rope(q_lin, sa.norm_q.weight, sa.norm_q.eps, geom["rope_cs"], d, q)
+        _lib.rmsnorm_rope(k_lin, sa.norm_k.weight, sa.norm_k.eps, geom["rope_cs"], d, k)
+        att_out = torch.empty(s, n, d, dtype=bf, device=dev)
+        bgh.run_blockgrid_hip(q.view(s, n, d), k.view(s, n, d), v.view(s, n, d), att_out,
+                              plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d)
+        y = sa.o(att_out.view(s, dim))
+        x1 = torch.empty_like(x)
+        _lib.residual_gate(x, y, mod[2], x1)
+
+        # cross-attention
+        xn = torch.empty_like(x)
+        _lib.ln_modulate(x1, self.norm3.weight, self.norm3.bias, None, None, self.norm3.eps, xn, a0)
+        xq, xs = quant_from(xn, a0)
+        cq = torch.empty(s, dim, dtype=bf, device=dev)
+        _lib.rmsnorm_rope(ca.q.gemm(xq, xs), ca.norm_q.weight, ca.norm_q.eps, None, d, cq)
+        lc = context.shape[0]
+        cxq, cxs = quantize_tensor(context, geom["amax_ctx"])
+        ck = torch.empty(lc, dim, dtype=bf, device=dev)
+        _lib.rmsnorm_rope(ca.k.gemm(cxq, cxs), ca.norm_k.weight, ca.norm_k.eps, None, d, ck)
+        cv = ca.v.gemm(cxq, cxs)
+        c_out = torch.empty(s, n, d, dtype=bf, device=dev)
+        geom["cross"].run(cq.view(s, n, d), ck.view(lc, n, d), cv.view(lc, n, d), c_out)
+        co = ca.o(c_out.view(s, dim))
+        x2 = torch.empty_like(x)
+        _lib.residual_gate(x1, co, geom["ones"], x2)
+
+        # FFN
+        ffn_in = torch.empty_like(x)
+        _lib.ln_modulate(x2, None, None, mod[4], mod[3], self.norm2.eps, ffn_in, a0)
+        xq, xs = quant_from(ffn_in, a0)
+        hmid = self.ffn[0].gemm(xq, xs, epilogue=1, amax_out=a1)
+        hq, hs = quant_from(hmid, a1)
+        y2 = self.ffn[2].gemm(hq, hs)
+        x3 = torch.empty_like(x)
+        _lib.residual_gate(x2, y2, mod[5], x3)
+        return x3
+
+
+#: Use the fused block forward when a block's Linears are all per-tensor Fp8Linear.
+FUSED = True
 
 
 class Head(nn.Module):
@@ -294,9 +380,16 @@ class SRDiT(nn.Module):
                                   bh=cfg.block_hw[0], bw=cfg.block_hw[1],
                                   rh=cfg.block_radius_hw[0], rw=cfg.block_radius_hw[1],
                                   sym_rt=cfg.sym_radius_t)
+        rope = rope_table(cfg, f, h, w, t_offset, device)
         return {"grid": (f, h, w), "plan": bgh.cached_plan(spec),
                 "cross": CrossAttentionPlan(f * h * w, lc),
-                "rope": rope_table(cfg, f, h, w, t_offset, device)}
+                "rope": rope,
+                # (cos, sin) pairs [s, head_dim/2] for the fused RMSNorm + RoPE kernel
+                "rope_cs": torch.view_as_real(rope).reshape(f * h * w, -1).contiguous(),
+                # amax words of the per-tensor quantisers, reused in stream order
+                "amax": torch.zeros(2, dtype=torch.int32, device=device),
+                "amax_ctx": torch.zeros(1, dtype=torch.int32, device=device),
+                "ones": torch.ones(cfg.dim, dtype=torch.float32, device=device)}
 
     # -- forward pieces -----------------------------------------------------
     def time_embed(self, t):

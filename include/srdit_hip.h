@@ -119,6 +119,58 @@ int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_row
                    const float* sb, int64_t sb_cols, const void* bias, void* out,
                    int64_t M, int64_t N, int64_t K, int64_t ldo, void* stream);
 
+/*
+ * The scaled fp8 GEMM with an epilogue: epilogue 0 stores bf16(v) as
+ * srdit_fp8_gemm does; epilogue 1 stores bf16(gelu_tanh(bf16(v))), the
+ * Linear's bf16 output fed to nn.GELU(approximate='tanh') as the FFN does
+ * (models.py:1200-1202).  amax_out (nullable, one uint32, device): cleared by
+ * the call, then set to the bits of max |out| for a per-tensor quantiser of
+ * the output (srdit_fp8_quant_apply).  Same layout rules as srdit_fp8_gemm.
+ */
+int srdit_fp8_gemm_ex(const void* a, const void* b, const float* sa, int64_t sa_rows,
+                      const float* sb, int64_t sb_cols, const void* bias, void* out,
+                      int64_t M, int64_t N, int64_t K, int64_t ldo, int epilogue,
+                      uint32_t* amax_out, void* stream);
+
+/*
+ * The quantise pass of srdit_fp8_quant_tensor alone: amax_ws already holds the
+ * bits of max |x| (written by a producer: srdit_ln_modulate or
+ * srdit_fp8_gemm_ex), scale[0] = max(amax * fl32(1/448), 1e-12) and
+ * xq = e4m3(clamp(x / scale, +-448)).
+ */
+int srdit_fp8_quant_apply(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype,
+                          void* xq, float* scale, const uint32_t* amax_ws, void* stream);
+
+/*
+ * Fused LayerNorm + adaLN modulation, one pass per row of x [M, K] (bf16):
+ *   y = bf16(LayerNorm(x; eps) [* ln_w + ln_b])      (ln_w, ln_b bf16 [K] or both NULL)
+ *   out = bf16(f32(y) * (1 + scale) + shift)          (scale, shift fp32 [K] or both NULL)
+ * WanLayerNorm (video_refiner/wan/modules/sr_dit/models.py:443-503) followed by
+ * the block's modulation (models.py:1308, :1258).  amax_ws (nullable): cleared,
+ * then max |out| bits, for srdit_fp8_quant_apply.  K % 8 == 0, 16-byte rows.
+ */
+int srdit_ln_modulate(const void* x, int64_t M, int K, int64_t ldx, const void* ln_w,
+                      const void* ln_b, const float* scale, const float* shift, float eps,
+                      void* out, int64_t ldo, uint32_t* amax_ws, void* stream);
+
+/*
+ * Gated residual: out = bf16(f32(x) + f32(y) * gate[k]) over [M, K] bf16,
+ * gate fp32 [K]; out may alias x.  The block's residual updates
+ * (models.py:1344, :1260).
+ */
+int srdit_residual_gate(const void* x, const void* y, const float* gate, int64_t M, int K,
+                        int64_t ldx, int64_t ldy, void* out, int64_t ldo, void* stream);
+
+/*
+ * RMSNorm over each row of x [M, K] (bf16, K = heads * head_dim) with weight w
+ * (bf16 [K]), then RoPE per head: pair j of a head rotated by
+ * (cos, sin) = rope_cs[row][j] (fp32 pairs, [M, head_dim/2]); rope_cs NULL skips
+ * the rotation (RMSNorm alone).  out [M, K] contiguous.  WanRMSNorm
+ * (models.py:424-440) then rope_apply (models.py:173-214).
+ */
+int srdit_rmsnorm_rope(const void* x, int64_t M, int K, int64_t ldx, const void* w, float eps,
+                       const float* rope_cs, int head_dim, void* out, void* stream);
+
 /* Message of the last failed call on this thread (NUL-terminated, truncated to
  * len).  Returns the message length. */
 int srdit_last_error(char* buf, int len);

@@ -164,3 +164,124 @@ def test_full_size_step_in_a_graph():
             torch.cuda.synchronize()
             assert torch.isfinite(y.float()).all()
             assert torch.equal(y, want), it
+
+
+def _bf16_close(got, ref, frac=1e-3, scale=None, atol=1e-30):
+    """Equal except in a small fraction of elements, which differ by at most one bf16
+    step of `scale` (default: the values themselves; pass the magnitude of the terms
+    when the result can cancel towards zero) plus `atol`."""
+    g, r = got.float(), ref.float()
+    diff = (g - r).abs()
+    mag = torch.maximum(r.abs(), g.abs()) if scale is None else scale
+    step = mag * 2 ** -7 + atol
+    assert (diff <= step).all(), float((diff / step).max())
+    assert (diff > 0).float().mean().item() <= frac, (diff > 0).float().mean().item()
+
+
+def test_fused_ln_modulate_and_amax():
+    from sr_dit import _lib
+    g = torch.Generator("cpu").manual_seed(5)
+    x = (torch.randn(700, 3072, generator=g) * 3 + 0.5).to(torch.bfloat16).to(DEV)
+    sc = (torch.randn(3072, generator=g) * 0.1).to(DEV)
+    sh = (torch.randn(3072, generator=g) * 0.1).to(DEV)
+    w = (torch.randn(3072, generator=g) * 0.5 + 1).to(torch.bfloat16).to(DEV)
+    b = (torch.randn(3072, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    out = torch.empty_like(x)
+    zero = torch.zeros(3072, device=DEV)
+    ln = F.layer_norm(x.float(), (3072,), None, None, 1e-6).to(torch.bfloat16)
+    _lib.ln_modulate(x, None, None, zero, zero, 1e-6, out, None)      # the LayerNorm stage alone
+    # (x - mean) cancels where x ~ mean, and the fp32 mean differs from torch's in
+    # its last bits: an absolute 1e-4 / 2^7 on these unit-variance outputs
+    _bf16_close(out, ln, atol=1e-4 * 2 ** -7)
+    amax = torch.full((1,), 7, dtype=torch.int32, device=DEV)
+    _lib.ln_modulate(x, None, None, sc, sh, 1e-6, out, amax)
+    ref = (ln.float() * (1 + sc) + sh).to(torch.bfloat16)
+    # a one-step change of the LayerNorm value moves the output by |ln (1 + sc)| / 2^8
+    _bf16_close(out, ref, scale=ln.float().abs() * (1 + sc).abs() + ref.float().abs(),
+                atol=1e-4 * 2 ** -7)
+    bits = out.float().abs().max().to(torch.float32).view(torch.int32)
+    assert amax.item() == bits.item()
+    _lib.ln_modulate(x, w, b, None, None, 1e-6, out, None)
+    ref = F.layer_norm(x.float(), (3072,), w.float(), b.float(), 1e-6).to(torch.bfloat16)
+    _bf16_close(out, ref, scale=ln.float().abs() * w.float().abs() + ref.float().abs(),
+                atol=1e-4 * 2 ** -7)
+
+
+def test_fused_residual_gate_bit_exact():
+    from sr_dit import _lib
+    g = torch.Generator("cpu").manual_seed(6)
+    x = torch.randn(513, 3072, generator=g).to(torch.bfloat16).to(DEV)
+    y = torch.randn(513, 3072, generator=g).to(torch.bfloat16).to(DEV)
+    gate = torch.randn(3072, generator=g).to(DEV)
+    out = torch.empty_like(x)
+    _lib.residual_gate(x, y, gate, out)
+    assert torch.equal(out, (x.float() + y.float() * gate).to(torch.bfloat16))
+    _lib.residual_gate(x, y, gate, x)          # in place
+    assert torch.equal(x, out)
+
+
+def test_fused_rmsnorm_rope():
+    from sr_dit import _lib
+    cfg = mdl.SRDiTConfig()
+    f, h, w = 2, 9, 10
+    s = f * h * w
+    g = torch.Generator("cpu").manual_seed(7)
+    x = (torch.randn(s, 9216, generator=g) * 2).to(torch.bfloat16).to(DEV)[:, 3072:6144]  # strided rows
+    wt = (torch.randn(3072, generator=g) * 0.3 + 1).to(torch.bfloat16).to(DEV)
+    tab = mdl.rope_table(cfg, f, h, w, 0, DEV)
+    cs = torch.view_as_real(tab).reshape(s, -1).contiguous()
+    out = torch.empty(s, 3072, dtype=torch.bfloat16, device=DEV)
+    _lib.rmsnorm_rope(x, wt, 1e-6, cs, 128, out)
+    xf = x.float()
+    y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * wt
+    ref = mdl.rope_apply(y.view(s, 24, 128), tab).view(s, 3072)
+    # a rotated pair can cancel: bound by the magnitude of the pair
+    yp = y.float().view(s, 1536, 2).abs().sum(-1, keepdim=True).expand(s, 1536, 2).reshape(s, 3072)
+    _bf16_close(out, ref, frac=2e-3, scale=yp)
+    _lib.rmsnorm_rope(x, wt, 1e-6, None, 128, out)
+    _bf16_close(out, y, frac=2e-3)
+
+
+def test_gemm_gelu_epilogue_and_amax():
+    from sr_dit import _lib
+    g = torch.Generator("cpu").manual_seed(8)
+    a = (torch.randn(300, 384, generator=g) * 0.5).to(F8).to(DEV)
+    b = (torch.randn(272, 384, generator=g) * 0.5).to(F8).to(DEV)
+    sa = torch.tensor([0.7], device=DEV)
+    sb = torch.tensor([1.3], device=DEV)
+    bias = (torch.randn(272, generator=g)).to(torch.bfloat16).to(DEV)
+    plain = torch.empty(300, 272, dtype=torch.bfloat16, device=DEV)
+    _lib.fp8_gemm(a, b, sa, sb, bias, plain)
+    out = torch.empty_like(plain)
+    amax = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _lib.fp8_gemm_ex(a, b, sa, sb, bias, out, epilogue=1, amax_out=amax)
+    # 1 + tanh(.) cancels for negative inputs: bound by the input's magnitude
+    _bf16_close(out, F.gelu(plain.float(), approximate="tanh").to(torch.bfloat16), frac=5e-3,
+                scale=plain.float().abs())
+    assert amax.item() == out.float().abs().max().view(torch.int32).item()
+    _lib.fp8_gemm_ex(a, b, sa, sb, bias, out, epilogue=0, amax_out=None)
+    assert torch.equal(out, plain)
+
+
+def test_fused_block_matches_unfused():
+    cfg = SMALL
+    model = mdl.build_refiner(cfg, device=DEV, scaling="tensor", seed=4)
+    f, h, w = 3, 16, 16
+    geom = model.geometry(f, h, w, cfg.text_len, DEV)
+    g = torch.Generator("cpu").manual_seed(1)
+    x = torch.randn(f * h * w, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+    ctx = torch.randn(cfg.text_len, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+    e0 = (torch.randn(1, 6, cfg.dim, generator=g) / cfg.dim ** 0.5).to(DEV)
+    with torch.no_grad():
+        assert all(b.fusable() for b in model.blocks)
+        fused = model.blocks_forward(x, e0, ctx, geom)
+        mdl.FUSED = False
+        try:
+            plain = model.blocks_forward(x, e0, ctx, geom)
+        finally:
+            mdl.FUSED = True
+    torch.cuda.synchronize()
+    err = (fused.float() - plain.float()).abs()
+    print(f"[metrics] fused vs op-by-op: max {err.max().item():.3e} mean {err.mean().item():.3e}",
+          flush=True)
+    assert err.mean().item() <= 2e-3 * plain.float().abs().mean().item()
