@@ -66,60 +66,6 @@ struct Tile {
   float mrun, lrun;    // running max (log2 units, lazily refreshed) and sum
 };
 
-// Per-lane LDS byte offsets, loop-invariant: the K A-operand reads, the V^T
-// transposing reads (lane part; the key-block part is a compile-time constant)
-// and the 16-byte chunk each fill load of this wavefront reads from its key's
-// head row (K swizzle for wavefront 0, V swizzle for wavefront 1).
-template <int D>
-struct LaneOff {
-  static constexpr int KS = D / 16, DT = D / 32, NL = D / 16;
-  int k[KS];
-  int v[DT];
-  int fill[NL];
-};
-
-// LDS tiles: 32 keys x D, one row of CPK 16-byte slots per key (chunk L = 8
-// head dims), row-major with an XOR swizzle of the slot within its row:
-//   slot(key, L) = key*CPK + (L ^ swz(key)).
-// Fill load q writes slots [64q, 64q + 64): lane l covers key 64q+l / CPK at
-// row position l % CPK, i.e. CPK consecutive lanes read one key's whole
-// contiguous head row (chunk (l % CPK) ^ swz(key)), so each load touches
-// 64/CPK full rows.  The swizzles (K: (key*CPK/16) % CPK; V: for D=128
-// 4(key%4) ^ 8((key>>2)&1), for D=64 key%8) make the K A-operand reads and the
-// V transposing reads hit every bank group equally often.
-template <int D> __device__ __forceinline__ int swz_k(int key) { return (key * (D / 8) / 16) % (D / 8); }
-template <int D> __device__ __forceinline__ int swz_v(int key) {
-  return D == 128 ? ((4 * (key & 3)) ^ (8 * ((key >> 2) & 1))) : (key % (D / 8));
-}
-
-template <int D>
-__device__ __forceinline__ LaneOff<D> make_lane_offsets(int wave) {
-  constexpr int CPK = D / 8, LPK = CPK, KPI = 64 / CPK;
-  LaneOff<D> o;
-  const int lane = threadIdx.x & 63;
-  const int c = lane & 31, hf = lane >> 5;
-  const int g = lane >> 4, i16 = lane & 15;
-#pragma unroll
-  for (int ks = 0; ks < LaneOff<D>::KS; ++ks)
-    o.k[ks] = (c * CPK + ((hf * LaneOff<D>::KS + ks) ^ swz_k<D>(c))) * 16;
-  // V^T read of (kk, dt, h2): key = 16kk + 8h2 + kl with kl = 4hf + i16/4; the
-  // swizzle of such a key depends on kl only, so the lane part is
-  // (kl*CPK + (Lc ^ swz_v(kl)))*16 + 8*(i16&1) and 16kk + 8h2 adds rows.
-  const int kl = 4 * hf + (i16 >> 2);
-#pragma unroll
-  for (int dt = 0; dt < LaneOff<D>::DT; ++dt) {
-    const int Lc = 4 * dt + 2 * (g & 1) + ((i16 & 3) >> 1);
-    o.v[dt] = (kl * CPK + (Lc ^ swz_v<D>(kl))) * 16 + 8 * (i16 & 1);
-  }
-  const int sub = (lane & 15) / LPK, pos = lane % CPK;
-#pragma unroll
-  for (int q = 0; q < LaneOff<D>::NL; ++q) {
-    const int key = q * KPI + (lane >> 4) * (16 / LPK) + sub;
-    o.fill[q] = (pos ^ (wave == 0 ? swz_k<D>(key) : swz_v<D>(key))) * 16;
-  }
-  return o;
-}
-
 // Token of key j of a run, walked forward KN keys per step: the lane keeps its
 // key's index within the current frame and that frame's first token.
 struct KeyCursor {

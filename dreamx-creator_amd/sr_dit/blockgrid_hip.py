@@ -246,12 +246,11 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     stride-1 head dim, on one device, bf16 or fp16.  The launch is
     asynchronous on the current stream.
 
-    ``kernel``: ``"auto"`` and ``"single"`` run the single-window kernel (two
-    32-query wavefronts per 64-query tile, two wavefronts per SIMD), the
-    faster one on every measured geometry; ``"grouped"`` runs the grouped
-    kernel (one 64-query member per wavefront, K/V fetches shared by paired
-    members), which needs plain rows without an anchor prefix and raises
-    otherwise.
+    ``kernel``: ``"auto"`` runs plain plans without an anchor prefix whose
+    64-query members pair well (>= 75% paired) on the grouped kernel (two
+    members per workgroup sharing their K/V fetches) and everything else on
+    the single-window kernel; ``"grouped"`` / ``"single"`` force one (a forced
+    grouped launch of an anchored plan raises).
     """
     for name, t in (("q", q), ("k_ext", k_ext), ("v_ext", v_ext), ("out", out)):
         if not t.is_cuda:
@@ -273,14 +272,20 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
         raise ValueError("run_blockgrid_hip: plan layout does not match anchor_mode.")
     if kernel not in ("auto", "grouped", "single"):
         raise ValueError(f"run_blockgrid_hip: kernel must be auto, grouped or single, got {kernel!r}")
-    use_grouped = kernel == "grouped"
-    if use_grouped and not groups_supported(plan):
+    if kernel == "grouped" and not groups_supported(plan):
         raise ValueError("run_blockgrid_hip: the grouped kernel needs plain rows without an anchor.")
-    if use_grouped:
+    use_grouped = False
+    if kernel != "single" and groups_supported(plan):
         key = ("groups", q.device)
         groups = plan.get(key)
         if groups is None:
-            groups = plan[key] = build_groups(plan).to(q.device)
+            host = build_groups(plan)
+            plan["groups_paired_fraction"] = paired_fraction(host)
+            groups = plan[key] = host.to(q.device)
+        # An unpaired member leaves two of its workgroup's four wavefronts
+        # idle; plans that pair poorly run faster on the single-window kernel.
+        use_grouped = kernel == "grouped" or plan["groups_paired_fraction"] >= 0.75
+    if use_grouped:
         _lib.window_attn_grouped_fwd(
             q, k_ext, v_ext, out, params, groups, n_w=plan["n_w"], n_groups=groups.shape[0],
             hr_base=hr_base, H=h, W=w, n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0],
