@@ -46,6 +46,10 @@ template <> struct Elem<__bf16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<h2, v8>(x); }
+  // a.x*b.x + a.y*b.y + c in fp32 (v_dot2_f32_bf16)
+  static __device__ __forceinline__ float dot2(h2 a, h2 b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
 };
 template <> struct Elem<_Float16> {
   typedef f16x8_t v8;
@@ -54,6 +58,10 @@ template <> struct Elem<_Float16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ v8 pack8(const float* x) { return pack8_impl<h2, v8>(x); }
+  // a.x*b.x + a.y*b.y + c in fp32 (v_dot2_f32_f16)
+  static __device__ __forceinline__ float dot2(h2 a, h2 b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+  }
 };
 
 // Largest growth (log2 units) of a query's running max tolerated before the

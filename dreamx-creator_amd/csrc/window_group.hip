@@ -46,6 +46,19 @@ struct GroupArgs {
 
 constexpr int GKN = 32;  // keys per block
 
+// 16 bytes per lane from record `index`, byte `offset` of the structured
+// buffer `rsrc` straight into LDS at byte address lds + 16 * lane
+// (buffer_load_dwordx4 ... idxen offen lds).  Written as inline asm so the
+// compiler does not treat it as an LDS store: it would otherwise wait for
+// every outstanding fill before any later LDS read.  The fills only ever
+// target the ring stage no wavefront is reading, and fill_barrier's explicit
+// full wait orders them before the reads of the next step.
+__device__ __forceinline__ void dma_x4(i32x4_t rsrc, uint32_t lds, int index, int offset) {
+  const i32x2_t va = {index, offset};
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 idxen offen lds" ::"v"(va), "s"(rsrc), "{m0}"(lds)
+               : "memory");
+}
+
 // The frames a member consumes in private slots: [lo1, lo1+len1) then
 // [lo2, lo2+len2) -- its frame range minus the frames shared with the partner.
 struct PrivFrames {
@@ -73,6 +86,16 @@ __device__ __forceinline__ int private_frame(const PrivFrames& p, int k) {
   return k < p.len2 ? p.lo2 + k : -1;
 }
 
+// Per-wavefront fill cursor: the step it fetches next and, per lane, the
+// row/column (within the spatial extent) of the key whose token the lane
+// decodes for the row broadcast.  Advancing one step adds 32 keys:
+// dq = 32 / kw_l rows and dr = 32 % kw_l columns, with one carry.
+struct FillCursor {
+  int fs, s;     // frame slot and spatial step of the next fill
+  int row, col;  // per lane
+  int fbase;     // token of (frame, kh0, kw0) for the current frame slot, -1: no frame
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   using E = Elem<T>;
@@ -84,6 +107,7 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   constexpr int LPK = CPK;        // fill lanes per key row
   constexpr int KPI = 64 / CPK;   // key rows per fill load
   constexpr int BLK = GKN * D;    // elements per block
+  constexpr int BLKB = BLK * static_cast<int>(sizeof(T));
   // [stage][block] rings: 2 stages x 2 blocks x 32 keys x D, for K and for V
   __shared__ __attribute__((aligned(16))) T ksh[4 * BLK];
   __shared__ __attribute__((aligned(16))) T vsh[4 * BLK];
@@ -114,12 +138,17 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   const int nsh = lb > 0 ? max(0, min(a0 + la, a1 + lb) - s_lo) : 0;
   const PrivFrames pf0 = private_frames(a0, la, s_lo, nsh);
   const PrivFrames pf1 = lb > 0 ? private_frames(a1, lb, s_lo, nsh) : PrivFrames{0, 0, 0, 0};
+  const PrivFrames pfm = member == 0 ? pf0 : pf1;
   const int P = max(la - nsh, lb > 0 ? lb - nsh : 0);
+  const int nslots = P + nsh;
   const int nS = (sp + GKN - 1) / GKN;
-  const int nsteps = (P + nsh) * nS;
-  const float r_kw = 1.0f / static_cast<float>(kw_l > 0 ? kw_l : 1);
-  auto slot_frame = [&](int w, int fs_) -> int {
-    return fs_ < P ? private_frame(w == 0 ? pf0 : pf1, fs_) : s_lo + (fs_ - P);
+  const int nsteps = nslots * nS;
+  const int first_shared = P * nS;  // steps before it are private (one block per member)
+  // This member's frame in slot fs_ (-1: none), without branches.
+  auto frame_of = [&](int fs_) __attribute__((always_inline)) -> int {
+    const int k2 = fs_ - pfm.len1;
+    const int fpriv = fs_ < pfm.len1 ? pfm.lo1 + fs_ : (k2 < pfm.len2 ? pfm.lo2 + k2 : -1);
+    return fs_ < P ? fpriv : (fs_ < nslots ? s_lo + (fs_ - P) : -1);
   };
 
   // This wavefront's 32 queries: rows m0 + 32*qhalf + [0, 32) of its member.
@@ -131,21 +160,36 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   const int lq = q_tl * q_sp;
   const int m0 = 64 * my_mt;
   const bool has_member = my_row >= 0 && qh_l > 0 && qw_l > 0 && q_tl > 0 && m0 >= 0 && m0 < lq;
+  // Slots this member consumes a block in, bit fs (the host limits a window
+  // to 16 KV frames, so a pair has at most 32 slots).
+  uint32_t act = 0;
+  if (has_member) {
+    for (int fs_ = 0; fs_ < nslots && fs_ < 32; ++fs_)
+      if (frame_of(fs_) >= 0) act |= 1u << fs_;
+  }
+  auto active = [&](int fs_) __attribute__((always_inline)) -> bool {
+    return ((act >> (fs_ & 31)) & 1u) != 0 && fs_ < 32;
+  };
 
   const int L = a.H * a.W;
   const int64_t tok = static_cast<int64_t>(a.n_heads) * D;
   const int tok_bytes = static_cast<int>(tok) * static_cast<int>(sizeof(T));
   const int kv_tokens = static_cast<int>(a.kv_tokens);
-  // K (even wavefronts) or V (odd) of this head as a structured buffer:
-  // record = token, stride = token stride in bytes.
-  const T* kvb = reinterpret_cast<const T*>(kv_role == 0 ? a.k : a.v) + head * D;
-  const __amdgpu_buffer_rsrc_t kvrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<T*>(kvb), static_cast<short>(tok_bytes), kv_tokens, 0x00020000);
+  // K (even wavefronts) or V (odd) of this head as a structured buffer
+  // (record = token, stride = token stride in bytes): base, base_hi |
+  // stride << 16, num_records, flags.
+  const uint64_t kva = reinterpret_cast<uint64_t>(reinterpret_cast<const T*>(kv_role == 0 ? a.k : a.v) +
+                                                  head * D);
+  const i32x4_t kvrsrc = {static_cast<int>(static_cast<uint32_t>(kva)),
+                          static_cast<int>(static_cast<uint32_t>(kva >> 32) |
+                                           (static_cast<uint32_t>(tok_bytes) << 16)),
+                          kv_tokens, 0x00020000};
+  const uint32_t lds_fill_base =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(kv_role == 0 ? ksh : vsh));
   const LaneOff<D> lo = make_lane_offsets<D>(kv_role);
 
   V8 qf[KS];
   f32x16_t oacc[DT];
-  float mrun = -INFINITY, lrun = 0.f;
   const int m = m0 + 32 * qhalf + c;
   const bool qvalid = has_member && m < lq;
   int64_t qflat;
@@ -167,90 +211,97 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
     for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16_t{};
   }
 
-  // Fill of step j into stage `stage`: block b of the step is fetched by
-  // wavefronts 2b (K) and 2b+1 (V).  Source lane s of a 16-lane row decodes
-  // the token of the key that load (s % LPK) places in that row; DPP
-  // row_newbcast hands it to the row.
+  // ---- fills ----------------------------------------------------------------
+  // Step t goes to stage t & 1.  In a private step block b holds member b's
+  // keys and is fetched by wavefronts 2b (K) and 2b+1 (V); in a shared step
+  // block 0 is fetched by wavefronts 0 and 1.  K is fetched two steps ahead of
+  // its use, V one step ahead.  Source lane s of a 16-lane row decodes the
+  // token of the key that load (s % LPK) places in that row; DPP row_newbcast
+  // hands it to the row.
   const int s16 = lane & 15;
   const int src_key = (s16 % LPK) * KPI + (lane >> 4) * (16 / LPK) + s16 / LPK;
   const int sub = s16 / LPK;
-  auto fill = [&](int j, int stage) {
-    const int fs_ = j / nS, s_ = j - fs_ * nS;
-    const int nblk = fs_ < P ? 2 : 1;
-    if (member >= nblk) return;  // uniform
-    const int f = slot_frame(member, fs_);
-    if (f < 0) return;           // uniform: the member has no frame in this slot
-    int idx = s_ * GKN + src_key;
-    idx = idx < sp ? idx : sp - 1;
-    const int row = fdiv(idx, kw_l, r_kw);
-    const int col = idx - row * kw_l;
-    int tokv = a.hr_base + f * L + __mul24(kh0 + row, a.W) + kw0 + col;
-    tokv = tokv < 0 ? 0 : (tokv >= kv_tokens ? kv_tokens - 1 : tokv);
-    T* dst = (kv_role == 0 ? ksh : vsh) + (stage * 2 + member) * BLK;
-    static_for<NL>([&](auto qc) {
-      constexpr int q = decltype(qc)::value;
-      int t = __builtin_amdgcn_mov_dpp(tokv, 0x150 + q, 0xf, 0xf, false);
-      if constexpr (LPK == 8) {
-        const int t1 = __builtin_amdgcn_mov_dpp(tokv, 0x150 + 8 + q, 0xf, 0xf, false);
-        t = sub ? t1 : t;
-      }
-      buffer_load_lds_x4(kvrsrc, dst + q * 512, t, lo.fill[q]);
-    });
+  const int kwl = kw_l > 0 ? kw_l : 1;
+  const int dq = GKN / kwl, dr = GKN - dq * kwl;
+  const int row_start = fdiv(src_key, kwl, 1.0f / static_cast<float>(kwl));
+  const int col_start = src_key - row_start * kwl;
+  const int last_tok = (kh_l - 1) * a.W + (kw_l - 1);  // last key of the extent, frame-relative
+  const int frame0_tok = a.hr_base + kh0 * a.W + kw0;
+  auto fbase_of = [&](int fs_) __attribute__((always_inline)) -> int {
+    const int f = frame_of(fs_);
+    return f >= 0 ? frame0_tok + f * L : -1;
+  };
+  FillCursor cur;
+  cur.fs = 0; cur.s = 0; cur.row = row_start; cur.col = col_start; cur.fbase = fbase_of(0);
+  const int look = kv_role == 0 ? 2 : 1;  // steps ahead this wavefront fetches
+  // Fetch the cursor's step into stage `stage` and advance, without branches
+  // except the one around the loads.
+  auto fill_next = [&](int stage) __attribute__((always_inline)) {
+    const bool priv = cur.fs < P;
+    if (__builtin_expect((priv || member == 0) && cur.fbase >= 0, 1)) {  // uniform
+      int t = cur.row < kh_l ? __mul24(cur.row, a.W) + cur.col : last_tok;
+      t += cur.fbase;
+      t = static_cast<int>(min(static_cast<uint32_t>(t), static_cast<uint32_t>(kv_tokens - 1)));
+      const uint32_t dst = lds_fill_base + static_cast<uint32_t>((stage * 2 + (priv ? member : 0)) * BLKB);
+      static_for<NL>([&](auto qc) __attribute__((always_inline)) {
+        constexpr int q = decltype(qc)::value;
+        int tq = __builtin_amdgcn_mov_dpp(t, 0x150 + q, 0xf, 0xf, false);
+        if constexpr (LPK == 8) {
+          const int t1 = __builtin_amdgcn_mov_dpp(t, 0x150 + 8 + q, 0xf, 0xf, false);
+          tq = sub ? t1 : tq;
+        }
+        dma_x4(kvrsrc, dst + q * 1024, tq, lo.fill[q]);
+      });
+    }
+    const bool wrap = cur.s + 1 == nS;
+    int r2 = cur.row + dq, c2 = cur.col + dr;
+    const bool carry = c2 >= kwl;
+    c2 -= carry ? kwl : 0;
+    r2 += carry ? 1 : 0;
+    cur.row = wrap ? row_start : r2;
+    cur.col = wrap ? col_start : c2;
+    cur.s = wrap ? 0 : cur.s + 1;
+    cur.fs += wrap ? 1 : 0;
+    const int fb = fbase_of(cur.fs);
+    cur.fbase = wrap ? fb : cur.fbase;
   };
 
-  // One step on stage `stage` (a compile-time constant, so the LDS addresses
-  // are lane offsets plus immediates).
-  auto step = [&](int j, int fs_, int s_, auto stage_c) {
+  // ---- compute --------------------------------------------------------------
+  // Iteration j issues the S^T MFMAs of step j+1 and then the softmax and P.V
+  // of step j, so the matrix core works on step j+1 while the vector ALU
+  // exponentiates step j.  ka/va are this wavefront's LDS lane offsets of the
+  // K block of step j+1 and the V block of step j (the member's own block in
+  // private steps, block 0 in shared ones); stages are immediates.
+  auto blk_off = [&](int t) __attribute__((always_inline)) -> int {
+    return (t < first_shared && member == 1) ? BLKB : 0;
+  };
+  int ka[KS], va[DT];
+  int koff = blk_off(0), voff = blk_off(0);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) ka[ks] = lo.k[ks] + koff;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) va[dt] = lo.v[dt] + voff;
+
+  struct KOps { V8 f[KS]; };
+  struct VOps { V8 t[2][DT]; };
+  auto read_k = [&](auto stage_c) __attribute__((always_inline)) -> KOps {
     constexpr int stage = decltype(stage_c)::value;
-    fill_barrier();  // fill j landed; step j-1's LDS reads retired in every wavefront
-    if (j + 1 < nsteps) fill(j + 1, stage ^ 1);
-    const int f = slot_frame(member, fs_);
-    if (!has_member || f < 0) return;  // uniform
-    const int blk = fs_ < P ? member : 0;
-    const char* kbuf = reinterpret_cast<const char*>(ksh + (stage * 2 + blk) * BLK);
-    const char* vbuf = reinterpret_cast<const char*>(vsh + (stage * 2 + blk) * BLK);
-
-    V8 kf[KS];
+    const char* kb = reinterpret_cast<const char*>(ksh) + stage * 2 * BLKB;
+    KOps r;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const V8*>(kbuf + lo.k[ks]);
-    f32x16_t sacc = f32x16_t{};
+    for (int ks = 0; ks < KS; ++ks) r.f[ks] = *reinterpret_cast<const V8*>(kb + ka[ks]);
+    return r;
+  };
+  auto s_mfma = [&](const KOps& kf) __attribute__((always_inline)) -> f32x16_t {
+    f32x16_t acc = E::mma(kf.f[0], qf[0], f32x16_t{});
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) sacc = E::mma(kf[ks], qf[ks], sacc);
-    __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);  // the K reads
-    __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);  // then the MFMAs
-
-    const int nvalid = sp - s_ * GKN;  // the last block of a frame can be partial
-    if (nvalid < GKN) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (key >= nvalid) sacc[r] = -INFINITY;
-      }
-    }
-    float mx = sacc[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
-    mx = other_half_max(mx) * a.scale_log2;
-    const bool up = mx > mrun + TAU;
-    if (__any(up)) {
-      const float alpha = up ? __builtin_amdgcn_exp2f(mrun - mx) : 1.0f;
-      lrun *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-      mrun = up ? mx : mrun;
-    }
-    const float msub = mrun == -INFINITY ? 0.f : mrun;
-    float pv[16];
-    float psum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], a.scale_log2, -msub));
-      psum += pv[r];
-    }
-    lrun += psum;
-    const V8 pf0 = E::pack8(&pv[0]);
-    const V8 pf1 = E::pack8(&pv[8]);
-    V8 vt[2][DT];
+    for (int ks = 1; ks < KS; ++ks) acc = E::mma(kf.f[ks], qf[ks], acc);
+    return acc;
+  };
+  auto read_v = [&](auto stage_c) __attribute__((always_inline)) -> VOps {
+    constexpr int stage = decltype(stage_c)::value;
+    const char* vb = reinterpret_cast<const char*>(vsh) + stage * 2 * BLKB;
+    VOps r;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
@@ -258,36 +309,152 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
         i32x2_t half[2];
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
-          const char* src = vbuf + (16 * kk + 8 * h2) * CPK * 16 + lo.v[dt];
+          const char* src = vb + (16 * kk + 8 * h2) * CPK * 16 + va[dt];
           half[h2] = __builtin_bit_cast(
               i32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(const_cast<char*>(src))));
         }
         const i32x4_t vw = {half[0][0], half[0][1], half[1][0], half[1][1]};
-        vt[kk][dt] = __builtin_bit_cast(V8, vw);
+        r.t[kk][dt] = __builtin_bit_cast(V8, vw);
       }
     }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt] = E::mma(vt[kk][dt], kk == 0 ? pf0 : pf1, oacc[dt]);
+    return r;
   };
 
-  if (nsteps > 0) fill(0, 0);
-  int fs = 0, s = 0;  // frame slot and spatial step of step j
-  auto advance = [&]() {
-    if (++s == nS) {
-      s = 0;
-      ++fs;
+  float lrun = 0.f;        // this lane's half of the row sum
+  float mrun = -INFINITY;  // running max (log2 units)
+  float neg_m = 0.f;       // -mrun once finite
+  float thr = -INFINITY;   // raw-score threshold (mrun + TAU) / scale_log2 for a rescale
+  const float inv_scale = 1.0f / a.scale_log2;
+  const typename E::h2 ones2 = {static_cast<T>(1.0f), static_cast<T>(1.0f)};
+
+  // Partial last block of a frame: keys >= nvalid never contribute.
+  auto mask_tail = [&](f32x16_t& sc, int nvalid) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (key >= nvalid) sc[r] = -INFINITY;
     }
+  };
+  // Running-max update (raw score units in, log2 units kept); rescales the
+  // accumulator when the max grew by more than TAU.
+  auto update_max = [&](const f32x16_t& sc) __attribute__((always_inline)) {
+    float mx = __builtin_fmaxf(sc[0], sc[1]);
+#pragma unroll
+    for (int r = 2; r < 16; ++r) mx = __builtin_fmaxf(mx, sc[r]);
+    mx = other_half_max(mx);
+    const bool up = mx > thr;
+    if (__builtin_expect(__any(up), 0)) {
+      const float mnew = mx * a.scale_log2;
+      const float alpha = up ? __builtin_amdgcn_exp2f(mrun - mnew) : 1.0f;
+      lrun *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      mrun = up ? mnew : mrun;
+      neg_m = -mrun;
+      thr = (mrun + TAU) * inv_scale;
+    }
+  };
+  // P = exp2(s * scale_log2 - m), rounded to T; the row sum adds the rounded
+  // values (the ones P.V uses), two per dot2.  Each packed word is copied to a
+  // scalar before its bit cast: clang casts element 0 for a bit cast of a
+  // vector element with a loop index.
+  auto exp_pack = [&](const f32x16_t& sc, V8& pa, V8& pb) __attribute__((always_inline)) {
+    float pv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], a.scale_log2, neg_m));
+    pa = E::pack8(&pv[0]);
+    pb = E::pack8(&pv[8]);
+    const i32x4_t wa = __builtin_bit_cast(i32x4_t, pa), wb = __builtin_bit_cast(i32x4_t, pb);
+    float ps = lrun;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w = wa[i];
+      ps = E::dot2(__builtin_bit_cast(typename E::h2, w), ones2, ps);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w = wb[i];
+      ps = E::dot2(__builtin_bit_cast(typename E::h2, w), ones2, ps);
+    }
+    lrun = ps;
+  };
+  auto pv_mfma = [&](const VOps& vt, const V8& pa, const V8& pb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] = E::mma(vt.t[0][dt], pa, oacc[dt]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] = E::mma(vt.t[1][dt], pb, oacc[dt]);
+  };
+
+  // Prologue: K of steps 0 and 1, V of step 0; S^T of step 0.
+  if (nsteps > 0) {
+    fill_next(0);
+    if (kv_role == 0 && nsteps > 1) fill_next(1);
+  }
+  fill_barrier();
+  f32x16_t s_cur = f32x16_t{};
+  if (nsteps > 0 && active(0)) s_cur = s_mfma(read_k(std::integral_constant<int, 0>{}));
+
+  int fs = 0, s = 0;  // frame slot and spatial step of step j
+  auto iteration = [&](int j, auto stage_c) __attribute__((always_inline)) {
+    constexpr int stage = decltype(stage_c)::value;  // stage of step j
+    fill_barrier();  // K of j+1 and V of j landed; iteration j-1's LDS reads retired everywhere
+    // K: step j+2 into stage j&1; V: step j+1 into stage (j+1)&1.
+    if (j + look < nsteps) fill_next(stage ^ (look & 1));
+    const bool wrap = s + 1 == nS;
+    const bool do_pv = active(fs);
+    const int nvalid = sp - s * GKN;
+    {
+      const int want = blk_off(j + 1);
+      if (__builtin_expect(want != koff, 0)) {  // uniform, once: private -> shared
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) ka[ks] += want - koff;
+        koff = want;
+      }
+    }
+    {
+      const int want = blk_off(j);
+      if (__builtin_expect(want != voff, 0)) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) va[dt] += want - voff;
+        voff = want;
+      }
+    }
+    // The S^T MFMAs run every iteration (on a stale block when the member has
+    // no frame in the next step's slot: that result is never consumed); the
+    // softmax and P.V only for an active step j.
+    const KOps kf = read_k(std::integral_constant<int, stage ^ 1>{});
+    f32x16_t s_next;
+    if (__builtin_expect(do_pv, 1)) {  // uniform
+      if (__builtin_expect(nvalid < GKN, 0)) mask_tail(s_cur, nvalid);
+      const VOps vt = read_v(std::integral_constant<int, stage>{});
+      update_max(s_cur);
+      // S^T MFMAs of step j+1 interleaved with the exponentials of step j,
+      // then P.V of step j interleaved with the conversions and row sums.
+      s_next = s_mfma(kf);
+      V8 pa, pb;
+      exp_pack(s_cur, pa, pb);
+      pv_mfma(vt, pa, pb);
+      static_for<KS>([&](auto) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+      });
+      static_for<2 * DT>([&](auto) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      });
+    } else {
+      s_next = s_mfma(kf);
+    }
+    s_cur = s_next;
+    fs += wrap ? 1 : 0;
+    s = wrap ? 0 : s + 1;
   };
   int j = 0;
   for (; j + 1 < nsteps; j += 2) {
-    step(j, fs, s, std::integral_constant<int, 0>{});
-    advance();
-    step(j + 1, fs, s, std::integral_constant<int, 1>{});
-    advance();
+    iteration(j, std::integral_constant<int, 0>{});
+    iteration(j + 1, std::integral_constant<int, 1>{});
   }
-  if (j < nsteps) step(j, fs, s, std::integral_constant<int, 0>{});
+  if (j < nsteps) iteration(j, std::integral_constant<int, 0>{});
 
   // O = acc / l ; lane (c, hf) writes dims dt*32 + 8*g4 + 4*hf + [0, 4) of its query
   const float lt = half_sum(lrun);
@@ -336,6 +503,8 @@ extern "C" int srdit_window_attn_grouped_fwd(const void* q, const void* k, const
   SRDIT_REQUIRE(static_cast<int64_t>(n_heads) * head_dim * 2 < (1LL << 14),
                 "srdit_window_attn_grouped_fwd: token stride n_heads*head_dim*2 must be below 16384 "
                 "bytes (structured-buffer stride)");
+  SRDIT_REQUIRE(scale > 0.f && scale < 1e30f,
+                "srdit_window_attn_grouped_fwd: softmax scale must be positive and finite");
   if (head_dim != 64 && head_dim != 128) {
     set_error("srdit_window_attn_grouped_fwd: head_dim %d unsupported (64 or 128)", head_dim);
     return SRDIT_EUNSUPPORTED;

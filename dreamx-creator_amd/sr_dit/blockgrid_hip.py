@@ -166,10 +166,13 @@ def longest_first_order(plan) -> torch.Tensor:
 
 
 def groups_supported(plan) -> bool:
-    """True when the grouped kernel can run the plan: plain rows, no anchor prefix."""
+    """True when the grouped kernel can run the plan: plain rows, no anchor
+    prefix, at most 16 KV frames per window (a pair walks at most 32 frame
+    slots)."""
     if plan["p_stride"] != P_PLAIN:
         return False
-    return bool((plan["params"][:, 12] == 0).all())
+    params = plan["params"]
+    return bool((params[:, 12] == 0).all()) and bool((params[:, 7] <= 16).all())
 
 
 def build_groups(plan) -> torch.Tensor:
