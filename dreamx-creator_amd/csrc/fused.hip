@@ -15,8 +15,8 @@
 // and add are contracted into an fma.  The reductions (mean, variance, mean of
 // squares) sum in a different order than torch's.
 //
-// One wavefront per row; a row is read from HBM once (later passes over it hit
-// L1/L2).  K % 8 == 0, rows 16-byte aligned.
+// One wavefront per row at a time; a row is read from HBM once.  K % 8 == 0,
+// rows 16-byte aligned.
 #include "common.h"
 
 namespace srdit {
@@ -65,69 +65,115 @@ __global__ void clear_word_kernel(uint32_t* p) { *p = 0u; }
 // LayerNorm over each row of x [M, K] (bf16, row stride ldx), eps, optional
 // affine (w, b bf16 [K]); then, with MOD, the adaLN modulation (scale, shift
 // fp32 [K]).  Output bf16 [M, K] with row stride ldo.
-template <bool AFFINE, bool MOD, bool AMAX>
+//
+// Each wavefront walks rows grid-stride.  With CACHED (K <= 4096) a lane
+// keeps its <= 8 chunks of the row in registers, so the row is read once;
+// otherwise the mean, variance and output passes re-read it (L1/L2 hits).
+// Per lane the chunks are summed in the order c = lane, lane + 64, ..., as the
+// output pass visits them.  The amax is reduced per workgroup, then one
+// atomicMax per workgroup.  VEC: scale and shift are 16-byte aligned and read
+// as float4.
+template <bool AFFINE, bool MOD, bool AMAX, bool CACHED, bool VEC>
 __global__ __launch_bounds__(256) void ln_modulate_kernel(
     const uint16_t* __restrict__ x, int64_t M, int K, int64_t ldx, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ b, const float* __restrict__ scale, const float* __restrict__ shift,
     float eps, uint16_t* __restrict__ out, int64_t ldo, uint32_t* __restrict__ amax_ws) {
+  constexpr int CPL = 8;  // cached chunks per lane
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= M) return;
-  const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
   const int nc = K >> 3;
-  float s = 0.f;
-  for (int c = lane; c < nc; c += 64) {
-    float f[8];
-    unpack_bf16x8(xr[c], f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s += f[i];
-  }
-  const float mean = wave_sum(s) / static_cast<float>(K);
-  float v = 0.f;
-  for (int c = lane; c < nc; c += 64) {
-    float f[8];
-    unpack_bf16x8(xr[c], f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float d = f[i] - mean;
-      v += d * d;
-    }
-  }
-  const float rstd = rsqrtf(wave_sum(v) / static_cast<float>(K) + eps);
-  uint4* orow = reinterpret_cast<uint4*>(out + row * ldo);
   uint32_t am = 0;
-  for (int c = lane; c < nc; c += 64) {
-    float f[8];
-    unpack_bf16x8(xr[c], f);
-    float wv[8], bv[8];
-    if (AFFINE) {
-      unpack_bf16x8(reinterpret_cast<const uint4*>(w)[c], wv);
-      unpack_bf16x8(reinterpret_cast<const uint4*>(b)[c], bv);
-    }
-    float o[8];
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < M;
+       row += static_cast<int64_t>(gridDim.x) * 4) {
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    uint4 rb[CACHED ? CPL : 1];
+    if (CACHED) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float y = __fmul_rn(f[i] - mean, rstd);
-      if (AFFINE) y = __fadd_rn(__fmul_rn(y, wv[i]), bv[i]);
-      y = bf16_round(y);  // LayerNorm(...).type_as(x)
-      if (MOD) {
-        const int k = 8 * c + i;
-        y = __fadd_rn(__fmul_rn(y, __fadd_rn(1.0f, scale[k])), shift[k]);
+      for (int i = 0; i < CPL; ++i) {
+        const int c = lane + 64 * i;
+        rb[i] = c < nc ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
       }
-      o[i] = y;
     }
-    const uint4 pk = pack_bf16x8(o);
-    orow[c] = pk;
-    if (AMAX) {
-      const uint32_t ww[4] = {pk.x, pk.y, pk.z, pk.w};
+    auto chunk = [&](int i, int c) -> uint4 { return CACHED ? rb[i] : xr[c]; };
+    float s = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        am = max(am, max((ww[i] & 0x7fffu) << 16, (ww[i] & 0x7fff0000u)));
+    for (int i = 0; i < (CACHED ? CPL : 1); ++i) {
+      for (int c = lane + 64 * i; c < nc && (CACHED || i == 0); c += (CACHED ? nc : 64)) {
+        float f[8];
+        unpack_bf16x8(chunk(i, c), f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += f[e];
+      }
+    }
+    const float mean = wave_sum(s) / static_cast<float>(K);
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < (CACHED ? CPL : 1); ++i) {
+      for (int c = lane + 64 * i; c < nc && (CACHED || i == 0); c += (CACHED ? nc : 64)) {
+        float f[8];
+        unpack_bf16x8(chunk(i, c), f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = f[e] - mean;
+          v += d * d;
+        }
+      }
+    }
+    const float rstd = rsqrtf(wave_sum(v) / static_cast<float>(K) + eps);
+    uint4* orow = reinterpret_cast<uint4*>(out + row * ldo);
+#pragma unroll
+    for (int i = 0; i < (CACHED ? CPL : 1); ++i) {
+      for (int c = lane + 64 * i; c < nc && (CACHED || i == 0); c += (CACHED ? nc : 64)) {
+        float f[8];
+        unpack_bf16x8(chunk(i, c), f);
+        float wv[8], bv[8], sv[8], hv[8];
+        if (AFFINE) {
+          unpack_bf16x8(reinterpret_cast<const uint4*>(w)[c], wv);
+          unpack_bf16x8(reinterpret_cast<const uint4*>(b)[c], bv);
+        }
+        if (MOD) {
+          if (VEC) {
+            const float4* s4 = reinterpret_cast<const float4*>(scale) + 2 * c;
+            const float4* h4 = reinterpret_cast<const float4*>(shift) + 2 * c;
+            const float4 s0 = s4[0], s1 = s4[1], h0 = h4[0], h1 = h4[1];
+            sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w;
+            sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
+            hv[0] = h0.x; hv[1] = h0.y; hv[2] = h0.z; hv[3] = h0.w;
+            hv[4] = h1.x; hv[5] = h1.y; hv[6] = h1.z; hv[7] = h1.w;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              sv[e] = scale[8 * c + e];
+              hv[e] = shift[8 * c + e];
+            }
+          }
+        }
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float y = __fmul_rn(f[e] - mean, rstd);
+          if (AFFINE) y = __fadd_rn(__fmul_rn(y, wv[e]), bv[e]);
+          y = bf16_round(y);  // LayerNorm(...).type_as(x)
+          if (MOD) y = __fadd_rn(__fmul_rn(y, __fadd_rn(1.0f, sv[e])), hv[e]);
+          o[e] = y;
+        }
+        const uint4 pk = pack_bf16x8(o);
+        orow[c] = pk;
+        if (AMAX) {
+          const uint32_t ww[4] = {pk.x, pk.y, pk.z, pk.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            am = max(am, max((ww[e] & 0x7fffu) << 16, (ww[e] & 0x7fff0000u)));
+        }
+      }
     }
   }
   if (AMAX) {
+    __shared__ uint32_t wmax[4];
     am = wave_umax(am);
-    if (lane == 0) atomicMax(amax_ws, am);
+    if (lane == 0) wmax[threadIdx.x >> 6] = am;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      atomicMax(amax_ws, max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3])));
   }
 }
 
@@ -234,14 +280,24 @@ extern "C" int srdit_ln_modulate(const void* x, int64_t M, int K, int64_t ldx, c
     clear_word_kernel<<<1, 1, 0, s>>>(amax_ws);
     SRDIT_LAUNCH_CHECK("clear_word_kernel");
   }
-  const unsigned blocks = static_cast<unsigned>((M + 3) / 4);
+  // Grid-stride over rows: at most 2048 workgroups of 4 row-wavefronts.
+  const int64_t want = (M + 3) / 4;
+  const unsigned blocks = static_cast<unsigned>(want < 2048 ? want : 2048);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(ln_w);
   const uint16_t* bp = static_cast<const uint16_t*>(ln_b);
   uint16_t* op = static_cast<uint16_t*>(out);
-#define SRDIT_LN_LAUNCH(A, MO, AM)                                                              \
-  ln_modulate_kernel<A, MO, AM><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, bp, scale, shift, eps, \
-                                                       op, ldo, amax_ws)
+  const bool cached = K <= 4096;
+  const bool vec = scale != nullptr && aligned16(scale) && aligned16(shift);
+#define SRDIT_LN_LAUNCH2(A, MO, AM, C, V)                                                      \
+  ln_modulate_kernel<A, MO, AM, C, V><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, bp, scale, shift, \
+                                                             eps, op, ldo, amax_ws)
+#define SRDIT_LN_LAUNCH(A, MO, AM)                                          \
+  do {                                                                       \
+    if (cached && vec) SRDIT_LN_LAUNCH2(A, MO, AM, true, true);              \
+    else if (cached) SRDIT_LN_LAUNCH2(A, MO, AM, true, false);               \
+    else SRDIT_LN_LAUNCH2(A, MO, AM, false, false);                          \
+  } while (0)
   const bool af = ln_w != nullptr, mo = scale != nullptr, am = amax_ws != nullptr;
   if (af && mo && am) SRDIT_LN_LAUNCH(true, true, true);
   else if (af && mo) SRDIT_LN_LAUNCH(true, true, false);
@@ -252,6 +308,7 @@ extern "C" int srdit_ln_modulate(const void* x, int64_t M, int K, int64_t ldx, c
   else if (am) SRDIT_LN_LAUNCH(false, false, true);
   else SRDIT_LN_LAUNCH(false, false, false);
 #undef SRDIT_LN_LAUNCH
+#undef SRDIT_LN_LAUNCH2
   SRDIT_LAUNCH_CHECK("ln_modulate_kernel");
   return SRDIT_OK;
 }
