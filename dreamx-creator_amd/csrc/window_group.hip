@@ -94,6 +94,8 @@ struct FillCursor {
   int fs, s;     // frame slot and spatial step of the next fill
   int row, col;  // per lane
   int fbase;     // token of (frame, kh0, kw0) for the current frame slot, -1: no frame
+  bool part;     // this wavefront fetches in the current frame slot
+  int blk;       // LDS byte offset of the slot's block within a stage
 };
 
 template <typename T, int D>
@@ -205,8 +207,16 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
     qflat = qflat < 0 ? 0 : (qflat >= a.q_tokens ? a.q_tokens - 1 : qflat);
     const V8* qp = reinterpret_cast<const V8*>(reinterpret_cast<const T*>(a.q) + head * D +
                                                qflat * tok + hf * (D / 2));
+    // Q enters the S^T MFMA pre-scaled by scale*log2(e) (rounded once to T),
+    // so the scores come out in log2 units.
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = qvalid ? qp[ks] : V8{};
+    for (int ks = 0; ks < KS; ++ks) {
+      const V8 raw = qvalid ? qp[ks] : V8{};
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(raw[i]) * a.scale_log2;
+      qf[ks] = E::pack8(x);
+    }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16_t{};
   }
@@ -232,17 +242,23 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
     return f >= 0 ? frame0_tok + f * L : -1;
   };
   FillCursor cur;
-  cur.fs = 0; cur.s = 0; cur.row = row_start; cur.col = col_start; cur.fbase = fbase_of(0);
-  const int look = kv_role == 0 ? 2 : 1;  // steps ahead this wavefront fetches
-  // Fetch the cursor's step into stage `stage` and advance, without branches
-  // except the one around the loads.
-  auto fill_next = [&](int stage) __attribute__((always_inline)) {
+  // Per-slot state of the cursor, refreshed when it enters a frame slot.
+  auto cursor_slot = [&]() __attribute__((always_inline)) {
     const bool priv = cur.fs < P;
-    if (__builtin_expect((priv || member == 0) && cur.fbase >= 0, 1)) {  // uniform
+    cur.fbase = fbase_of(cur.fs);
+    cur.part = (priv || member == 0) && cur.fbase >= 0;
+    cur.blk = priv ? member * BLKB : 0;
+  };
+  cur.fs = 0; cur.s = 0; cur.row = row_start; cur.col = col_start;
+  cursor_slot();
+  const int look = kv_role == 0 ? 2 : 1;  // steps ahead this wavefront fetches
+  // Fetch the cursor's step into stage `stage` and advance.
+  auto fill_next = [&](int stage) __attribute__((always_inline)) {
+    if (__builtin_expect(cur.part, 1)) {  // uniform
       int t = cur.row < kh_l ? __mul24(cur.row, a.W) + cur.col : last_tok;
       t += cur.fbase;
       t = static_cast<int>(min(static_cast<uint32_t>(t), static_cast<uint32_t>(kv_tokens - 1)));
-      const uint32_t dst = lds_fill_base + static_cast<uint32_t>((stage * 2 + (priv ? member : 0)) * BLKB);
+      const uint32_t dst = lds_fill_base + static_cast<uint32_t>(stage * 2 * BLKB + cur.blk);
       static_for<NL>([&](auto qc) __attribute__((always_inline)) {
         constexpr int q = decltype(qc)::value;
         int tq = __builtin_amdgcn_mov_dpp(t, 0x150 + q, 0xf, 0xf, false);
@@ -253,17 +269,19 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
         dma_x4(kvrsrc, dst + q * 1024, tq, lo.fill[q]);
       });
     }
-    const bool wrap = cur.s + 1 == nS;
-    int r2 = cur.row + dq, c2 = cur.col + dr;
-    const bool carry = c2 >= kwl;
-    c2 -= carry ? kwl : 0;
-    r2 += carry ? 1 : 0;
-    cur.row = wrap ? row_start : r2;
-    cur.col = wrap ? col_start : c2;
-    cur.s = wrap ? 0 : cur.s + 1;
-    cur.fs += wrap ? 1 : 0;
-    const int fb = fbase_of(cur.fs);
-    cur.fbase = wrap ? fb : cur.fbase;
+    if (__builtin_expect(++cur.s == nS, 0)) {  // uniform: next frame slot
+      cur.s = 0;
+      ++cur.fs;
+      cur.row = row_start;
+      cur.col = col_start;
+      cursor_slot();
+    } else {
+      cur.row += dq;
+      cur.col += dr;
+      const bool carry = cur.col >= kwl;
+      cur.col -= carry ? kwl : 0;
+      cur.row += carry ? 1 : 0;
+    }
   };
 
   // ---- compute --------------------------------------------------------------
@@ -292,12 +310,6 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
     for (int ks = 0; ks < KS; ++ks) r.f[ks] = *reinterpret_cast<const V8*>(kb + ka[ks]);
     return r;
   };
-  auto s_mfma = [&](const KOps& kf) __attribute__((always_inline)) -> f32x16_t {
-    f32x16_t acc = E::mma(kf.f[0], qf[0], f32x16_t{});
-#pragma unroll
-    for (int ks = 1; ks < KS; ++ks) acc = E::mma(kf.f[ks], qf[ks], acc);
-    return acc;
-  };
   auto read_v = [&](auto stage_c) __attribute__((always_inline)) -> VOps {
     constexpr int stage = decltype(stage_c)::value;
     const char* vb = reinterpret_cast<const char*>(vsh) + stage * 2 * BLKB;
@@ -320,13 +332,24 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
     return r;
   };
 
+  // Softmax state.  The running max m (log2 units) is subtracted inside the
+  // S^T MFMA: its C input holds -m in every slot, so the MFMA yields s - m.
+  // m is set from the first active block and raised only when a block's P
+  // would pass PMAX (its row sum exceeds PMAX, or is not finite); between
+  // raises P = exp2(s - m) <= PMAX, which the final O = acc / l cancels.
+  constexpr float PMAX = 4294967296.0f;  // 2^32
   float lrun = 0.f;        // this lane's half of the row sum
-  float mrun = -INFINITY;  // running max (log2 units)
-  float neg_m = 0.f;       // -mrun once finite
-  float thr = -INFINITY;   // raw-score threshold (mrun + TAU) / scale_log2 for a rescale
-  const float inv_scale = 1.0f / a.scale_log2;
+  float mrun = 0.f;        // running max, valid once minit
+  bool minit = false;      // wave-uniform: m has been set
+  f32x16_t cneg = f32x16_t{};
   const typename E::h2 ones2 = {static_cast<T>(1.0f), static_cast<T>(1.0f)};
 
+  auto s_mfma = [&](const KOps& kf) __attribute__((always_inline)) -> f32x16_t {
+    f32x16_t acc = E::mma(kf.f[0], qf[0], cneg);
+#pragma unroll
+    for (int ks = 1; ks < KS; ++ks) acc = E::mma(kf.f[ks], qf[ks], acc);
+    return acc;
+  };
   // Partial last block of a frame: keys >= nvalid never contribute.
   auto mask_tail = [&](f32x16_t& sc, int nvalid) __attribute__((always_inline)) {
 #pragma unroll
@@ -335,37 +358,24 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
       if (key >= nvalid) sc[r] = -INFINITY;
     }
   };
-  // Running-max update (raw score units in, log2 units kept); rescales the
-  // accumulator when the max grew by more than TAU.
-  auto update_max = [&](const f32x16_t& sc) __attribute__((always_inline)) {
+  auto row_max = [&](const f32x16_t& sc) __attribute__((always_inline)) -> float {
     float mx = __builtin_fmaxf(sc[0], sc[1]);
 #pragma unroll
     for (int r = 2; r < 16; ++r) mx = __builtin_fmaxf(mx, sc[r]);
-    mx = other_half_max(mx);
-    const bool up = mx > thr;
-    if (__builtin_expect(__any(up), 0)) {
-      const float mnew = mx * a.scale_log2;
-      const float alpha = up ? __builtin_amdgcn_exp2f(mrun - mnew) : 1.0f;
-      lrun *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-      mrun = up ? mnew : mrun;
-      neg_m = -mrun;
-      thr = (mrun + TAU) * inv_scale;
-    }
+    return other_half_max(mx);  // both key halves of the query
   };
-  // P = exp2(s * scale_log2 - m), rounded to T; the row sum adds the rounded
-  // values (the ones P.V uses), two per dot2.  Each packed word is copied to a
-  // scalar before its bit cast: clang casts element 0 for a bit cast of a
-  // vector element with a loop index.
-  auto exp_pack = [&](const f32x16_t& sc, V8& pa, V8& pb) __attribute__((always_inline)) {
+  // P = exp2(sc) rounded to T, and the sum of the rounded values (the ones
+  // P.V uses), two per dot2.  Each packed word is copied to a scalar before
+  // its bit cast: clang casts element 0 for a bit cast of a vector element
+  // with a loop index.
+  auto exp_pack = [&](const f32x16_t& sc, V8& pa, V8& pb) __attribute__((always_inline)) -> float {
     float pv[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], a.scale_log2, neg_m));
+    for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(sc[r]);
     pa = E::pack8(&pv[0]);
     pb = E::pack8(&pv[8]);
     const i32x4_t wa = __builtin_bit_cast(i32x4_t, pa), wb = __builtin_bit_cast(i32x4_t, pb);
-    float ps = lrun;
+    float ps = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int w = wa[i];
@@ -376,7 +386,15 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
       const int w = wb[i];
       ps = E::dot2(__builtin_bit_cast(typename E::h2, w), ones2, ps);
     }
-    lrun = ps;
+    return ps;
+  };
+  auto shift = [&](f32x16_t& sc, float d) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[r] -= d;
+  };
+  auto set_cneg = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) cneg[r] = -mrun;
   };
   auto pv_mfma = [&](const VOps& vt, const V8& pa, const V8& pb) __attribute__((always_inline)) {
 #pragma unroll
@@ -395,29 +413,22 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   if (nsteps > 0 && active(0)) s_cur = s_mfma(read_k(std::integral_constant<int, 0>{}));
 
   int fs = 0, s = 0;  // frame slot and spatial step of step j
+  bool do_pv = nsteps > 0 && active(0);  // the member consumes step j
+  const int tail_valid = sp - (nS - 1) * GKN;  // keys of a frame's last block
   auto iteration = [&](int j, auto stage_c) __attribute__((always_inline)) {
     constexpr int stage = decltype(stage_c)::value;  // stage of step j
     fill_barrier();  // K of j+1 and V of j landed; iteration j-1's LDS reads retired everywhere
     // K: step j+2 into stage j&1; V: step j+1 into stage (j+1)&1.
     if (j + look < nsteps) fill_next(stage ^ (look & 1));
-    const bool wrap = s + 1 == nS;
-    const bool do_pv = active(fs);
-    const int nvalid = sp - s * GKN;
-    {
-      const int want = blk_off(j + 1);
-      if (__builtin_expect(want != koff, 0)) {  // uniform, once: private -> shared
+    // private -> shared: the K block of step j+1 and the V block of step j
+    // move to block 0 (once each; member 1 only)
+    if (__builtin_expect(j + 1 == first_shared && member == 1, 0)) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) ka[ks] += want - koff;
-        koff = want;
-      }
+      for (int ks = 0; ks < KS; ++ks) ka[ks] -= BLKB;
     }
-    {
-      const int want = blk_off(j);
-      if (__builtin_expect(want != voff, 0)) {
+    if (__builtin_expect(j == first_shared && member == 1 && j > 0, 0)) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) va[dt] += want - voff;
-        voff = want;
-      }
+      for (int dt = 0; dt < DT; ++dt) va[dt] -= BLKB;
     }
     // The S^T MFMAs run every iteration (on a stale block when the member has
     // no frame in the next step's slot: that result is never consumed); the
@@ -425,29 +436,50 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
     const KOps kf = read_k(std::integral_constant<int, stage ^ 1>{});
     f32x16_t s_next;
     if (__builtin_expect(do_pv, 1)) {  // uniform
-      if (__builtin_expect(nvalid < GKN, 0)) mask_tail(s_cur, nvalid);
+      if (__builtin_expect(s == nS - 1 && tail_valid < GKN, 0)) mask_tail(s_cur, tail_valid);
       const VOps vt = read_v(std::integral_constant<int, stage>{});
-      update_max(s_cur);
+      if (__builtin_expect(!minit, 0)) {  // first active block: m = its row max
+        mrun = row_max(s_cur);
+        shift(s_cur, mrun);
+        set_cneg();
+        minit = true;
+      }
       // S^T MFMAs of step j+1 interleaved with the exponentials of step j,
       // then P.V of step j interleaved with the conversions and row sums.
       s_next = s_mfma(kf);
       V8 pa, pb;
-      exp_pack(s_cur, pa, pb);
+      float ps = exp_pack(s_cur, pa, pb);
+      if (__builtin_expect(__any(!(ps <= PMAX)), 0)) {  // raise m (rare)
+        const float d = fmaxf(row_max(s_cur), 0.f);
+        const float alpha = __builtin_amdgcn_exp2f(-d);
+        lrun *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        mrun += d;
+        set_cneg();
+        shift(s_cur, d);
+        shift(s_next, d);  // issued with the old m
+        ps = exp_pack(s_cur, pa, pb);
+      }
+      lrun += ps;
       pv_mfma(vt, pa, pb);
       static_for<KS>([&](auto) __attribute__((always_inline)) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
       });
       static_for<2 * DT>([&](auto) __attribute__((always_inline)) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
       });
     } else {
       s_next = s_mfma(kf);
     }
     s_cur = s_next;
-    fs += wrap ? 1 : 0;
-    s = wrap ? 0 : s + 1;
+    if (__builtin_expect(++s == nS, 0)) {  // uniform: next frame slot
+      s = 0;
+      ++fs;
+      do_pv = active(fs);
+    }
   };
   int j = 0;
   for (; j + 1 < nsteps; j += 2) {
