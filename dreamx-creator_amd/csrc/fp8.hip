@@ -445,6 +445,8 @@ extern "C" int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64
 }
 
 namespace srdit {
+int lt_fp8_gemm(const void* a, const void* b, const float* sa, const float* sb, const void* bias,
+                void* out, int64_t M, int64_t N, int64_t K, int64_t ldo, hipStream_t stream);
 namespace {
 int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_rows, const float* sb,
                     int64_t sb_cols, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
@@ -465,8 +467,15 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
   SRDIT_REQUIRE(aligned16(a) && aligned16(b) && aligned16(sb) && aligned16(out) &&
                     (!bias || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0),
                 "%s: a, b, sb, out must be 16-byte aligned and bias 8-byte aligned", who);
+  const bool force_mfma = (epilogue & SRDIT_GEMM_MFMA) != 0;
+  epilogue &= ~SRDIT_GEMM_MFMA;
   SRDIT_REQUIRE(epilogue == 0 || epilogue == 1, "%s: epilogue %d is not 0 (none) or 1 (gelu)", who,
                 epilogue);
+  // Plain GEMMs with per-tensor scales go to hipBLASLt; the MFMA kernel below
+  // runs the fused epilogues, row-wise scales and what hipBLASLt declines.
+  if (!force_mfma && epilogue == 0 && !amax_out && sa_rows == 1 && sb_cols == 1 &&
+      lt_fp8_gemm(a, b, sa, sb, bias, out, M, N, K, ldo, static_cast<hipStream_t>(stream)) == 0)
+    return SRDIT_OK;
   GemmArgs g;
   g.a = static_cast<const uint8_t*>(a);
   g.b = static_cast<const uint8_t*>(b);

@@ -1,0 +1,128 @@
+// Plain fp8 GEMMs through hipBLASLt: out = bf16(sa * sb * (a . b^T) + bias)
+// with per-tensor scales, the case of every Linear of the refiner block that
+// has no fused epilogue.  The hand-written MFMA kernel (fp8.hip) covers the
+// fused epilogues and row-wise scales, and any shape hipBLASLt declines.
+//
+// Layout: a [M, K] e4m3 row-major (activations), b [N, K] e4m3 row-major (the
+// nn.Linear weight), out [M, N] bf16 row-major with row stride ldo.  In
+// column-major terms out^T [N, M] = b . a^T: A = b with op T (a [K, N]
+// column-major matrix), B = a with op N ([K, M]), D = out^T with ld = ldo.
+// The weight scale is A's scale, the activation scale B's.
+//
+// One handle per device; a descriptor, layouts and the heuristic's first
+// algorithm are kept per (device, M, N, K, ldo, bias) and reused.  No
+// workspace is given to hipBLASLt, so a call allocates nothing and launches
+// only kernels (it can be captured in a HIP graph).
+#include "common.h"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+namespace srdit {
+
+namespace {
+
+struct LtPlan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  bool ok = false;
+};
+
+struct LtState {
+  std::mutex mu;
+  std::map<int, hipblasLtHandle_t> handles;
+  std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, bool>, LtPlan> plans;
+};
+
+LtState& lt_state() {
+  static LtState* s = new LtState();  // lives until the process ends
+  return *s;
+}
+
+bool lt_ok(hipblasStatus_t st) { return st == HIPBLAS_STATUS_SUCCESS; }
+
+bool make_plan(hipblasLtHandle_t h, LtPlan& p, int64_t M, int64_t N, int64_t K, int64_t ldo,
+               bool bias) {
+  if (!lt_ok(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F))) return false;
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  if (!lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta))) ||
+      !lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb))))
+    return false;
+  if (bias) {
+    const hipblasLtEpilogue_t epi = HIPBLASLT_EPILOGUE_BIAS;
+    const int32_t bt = HIP_R_16BF;
+    if (!lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi,
+                                               sizeof(epi))) ||
+        !lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt,
+                                               sizeof(bt))))
+      return false;
+  }
+  if (!lt_ok(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_8F_E4M3, K, N, K)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_8F_E4M3, K, M, K)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p.ld, HIP_R_16BF, N, M, ldo)))
+    return false;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (!lt_ok(hipblasLtMatmulPreferenceCreate(&pref))) return false;
+  const uint64_t ws = 0;
+  hipblasLtMatmulHeuristicResult_t res{};
+  int count = 0;
+  const bool got =
+      lt_ok(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                  &ws, sizeof(ws))) &&
+      lt_ok(hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.ld, p.ld, pref, 1, &res,
+                                            &count)) &&
+      count > 0 && lt_ok(res.state) && res.workspaceSize == 0;
+  hipblasLtMatmulPreferenceDestroy(pref);
+  if (!got) return false;
+  p.algo = res.algo;
+  return true;
+}
+
+}  // namespace
+
+// 0 when hipBLASLt ran the GEMM; nonzero when it declined (the caller then
+// runs the MFMA kernel).  sa and sb are single fp32 scales in device memory.
+int lt_fp8_gemm(const void* a, const void* b, const float* sa, const float* sb, const void* bias,
+                void* out, int64_t M, int64_t N, int64_t K, int64_t ldo, hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  LtState& st = lt_state();
+  std::lock_guard<std::mutex> guard(st.mu);
+  auto hit = st.handles.find(dev);
+  if (hit == st.handles.end()) {
+    hipblasLtHandle_t h = nullptr;
+    if (!lt_ok(hipblasLtCreate(&h))) h = nullptr;
+    hit = st.handles.emplace(dev, h).first;
+  }
+  hipblasLtHandle_t h = hit->second;
+  if (!h) return 2;
+  const auto key = std::make_tuple(dev, M, N, K, ldo, bias != nullptr);
+  auto pit = st.plans.find(key);
+  if (pit == st.plans.end()) {
+    LtPlan p;
+    p.ok = make_plan(h, p, M, N, K, ldo, bias != nullptr);
+    pit = st.plans.emplace(key, p).first;
+  }
+  LtPlan& p = pit->second;
+  if (!p.ok) return 3;
+  const void* scale_a = sb;  // the weight is hipBLASLt's A
+  const void* scale_b = sa;
+  if (!lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_A_SCALE_POINTER,
+                                             &scale_a, sizeof(scale_a))) ||
+      !lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_B_SCALE_POINTER,
+                                             &scale_b, sizeof(scale_b))))
+    return 4;
+  if (bias && !lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER,
+                                                     &bias, sizeof(bias))))
+    return 5;
+  const float alpha = 1.0f, beta = 0.0f;
+  const hipblasStatus_t rs = hipblasLtMatmul(h, p.desc, &alpha, b, p.la, a, p.lb, &beta, out, p.ld,
+                                             out, p.ld, &p.algo, nullptr, 0, stream);
+  return lt_ok(rs) ? 0 : 6;
+}
+
+}  // namespace srdit

@@ -83,7 +83,9 @@ def build(verbose: bool = False) -> str:
                      f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
     _run(cmds, verbose)
     tmp = OUT + ".tmp"
-    _run([[cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]], verbose)
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    _run([[cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, f"-L{rocm}/lib", "-lhipblaslt",
+           f"-Wl,-rpath,{rocm}/lib", "-o", tmp]], verbose)
     os.replace(tmp, OUT)
     return OUT
 

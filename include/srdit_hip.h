@@ -127,6 +127,10 @@ int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_row
  * the call, then set to the bits of max |out| for a per-tensor quantiser of
  * the output (srdit_fp8_quant_apply).  Same layout rules as srdit_fp8_gemm.
  */
+/* Flag for the epilogue argument of srdit_fp8_gemm_ex: run the hand-written
+ * MFMA kernel even where the plain-GEMM library path would be taken. */
+#define SRDIT_GEMM_MFMA 0x100
+
 int srdit_fp8_gemm_ex(const void* a, const void* b, const float* sa, int64_t sa_rows,
                       const float* sb, int64_t sb_cols, const void* bias, void* out,
                       int64_t M, int64_t N, int64_t K, int64_t ldo, int epilogue,

@@ -145,6 +145,52 @@ def test_gemm_matches_dequantised_product(M, N, K, rs, cs, use_bias):
     _gemm_check(out, a, b, sa, sb, bias.float().numpy() if bias is not None else None)
 
 
+TENSOR_CASES = [
+    # M, N, K, bias, ldo (None: N)
+    (64, 32, 256, False, None),
+    (300, 272, 384, True, None),
+    (1, 16, 128, True, None),
+    (96, 48, 256, True, 64),
+    (1000, 3072, 3072, True, None),
+    (21600, 3072, 3072, True, None),
+]
+
+
+@pytest.mark.parametrize("backend", ["auto", "mfma"])
+@pytest.mark.parametrize("M,N,K,use_bias,ldo", TENSOR_CASES, ids=lambda v: str(v))
+def test_gemm_per_tensor_both_backends(M, N, K, use_bias, ldo, backend):
+    """Per-tensor scales: the plain-GEMM library path ("auto") and the MFMA
+    kernel, each against the dequantised product with the per-element bound;
+    padding columns of a strided output stay untouched."""
+    print(f"gemm per-tensor {backend} M={M} N={N} K={K} bias={use_bias} ldo={ldo}", flush=True)
+    a, _ = _quant_codes((M, K), seed=M + 2 * K)
+    b, _ = _quant_codes((N, K), seed=N + 5 * K)
+    sa, sb = np.float32([0.75]), np.float32([1.25 / 64])
+    g = torch.Generator("cpu").manual_seed(9)
+    bias = (torch.randn(N, generator=g) * 4).to(torch.bfloat16) if use_bias else None
+    lo = ldo or N
+    buf = torch.full((M, lo), 7.0, dtype=torch.bfloat16, device="cuda")
+    out = buf[:, :N]
+    _lib().fp8_gemm_ex(torch.from_numpy(a).view(F8).cuda(), torch.from_numpy(b).view(F8).cuda(),
+                       torch.from_numpy(sa).cuda(), torch.from_numpy(sb).cuda(),
+                       bias.cuda() if bias is not None else None, out,
+                       force_mfma=(backend == "mfma"))
+    torch.cuda.synchronize()
+    if M * N <= 4_000_000:
+        _gemm_check(out, a, b, sa, sb, bias.float().numpy() if bias is not None else None)
+    else:  # production size: torch fp32 matmul of the dequantised operands
+        torch.backends.cuda.matmul.allow_tf32 = False
+        t = torch.from_numpy(of.e4m3_decode_table()).float().cuda()
+        A, B = t[torch.from_numpy(a).cuda().long()], t[torch.from_numpy(b).cuda().long()]
+        ref = (A @ B.T) * float(sa[0]) * float(sb[0]) + bias.float().cuda()
+        absum = (A.abs() @ B.abs().T) * float(sa[0]) * float(sb[0])
+        tol = 2.0 ** -8 * ref.abs() + 2.0 ** -12 * absum + 2.0 ** -20 * absum.max()
+        worst = ((out.float() - ref).abs() / tol).max().item()
+        assert worst <= 1.0, worst
+    if lo > N:
+        assert torch.all(buf[:, N:] == 7.0)
+
+
 def test_gemm_strided_output_leaves_padding():
     M, N, K, ldo = 96, 48, 256, 64
     a, sa = _quant_codes((M, K), seed=1)
