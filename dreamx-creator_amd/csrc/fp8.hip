@@ -217,6 +217,63 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
+// bf16 round trip (nearest even): the value torch holds after .to(bf16).
+__device__ __forceinline__ float bf16_rt(float x) {
+  typedef float f32x2v __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+  const uint32_t b = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{x, 0.f}, bf16x2v));
+  return __uint_as_float(b << 16);
+}
+
+// The FFN's hidden activation h = bf16(gelu_tanh(x)) for x [M, K] bf16 (the
+// first Linear's bf16 output), quantised per tensor without storing h: pass 1
+// reduces max |h| into amax_ws, pass 2 recomputes h and writes its e4m3 codes
+// and the scale, exactly as the per-tensor quantiser of a stored h would.
+__global__ __launch_bounds__(256) void gelu_amax_kernel(const uint16_t* __restrict__ x, int64_t M,
+                                                        int64_t K, int64_t ldx,
+                                                        uint32_t* __restrict__ amax_ws) {
+  __shared__ uint32_t part[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t nchunk = K >> 3;
+  uint32_t amax = 0;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
+    const uint16_t* xr = x + row * ldx;
+    for (int64_t c = lane; c < nchunk; c += 64) {
+      float f[8];
+      Load8<uint16_t>::get(xr, c, f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = bf16_rt(gelu_tanh(f[i]));
+      amax = abs_bits_max8(f, amax);
+    }
+  }
+  amax = wave_umax(amax);
+  if (lane == 0) part[wave] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicMax(amax_ws, max(max(part[0], part[1]), max(part[2], part[3])));
+}
+
+__global__ __launch_bounds__(256) void gelu_quant_kernel(const uint16_t* __restrict__ x, int64_t M,
+                                                         int64_t K, int64_t ldx,
+                                                         uint8_t* __restrict__ xq,
+                                                         float* __restrict__ scale,
+                                                         const uint32_t* __restrict__ amax_ws) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float s = scale_from_amax_bits(*amax_ws);
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
+  const int64_t nchunk = K >> 3;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
+    const uint16_t* xr = x + row * ldx;
+    uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
+    for (int64_t c = lane; c < nchunk; c += 64) {
+      float f[8];
+      Load8<uint16_t>::get(xr, c, f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = bf16_rt(gelu_tanh(f[i]));
+      qr[c] = to_e4m3x8(f, s);
+    }
+  }
+}
+
 // EPI 0: out = bf16(v); EPI 1: out = bf16(gelu(bf16(v))), the Linear's bf16
 // output fed to nn.GELU(approximate='tanh').  AMAX: also the max |out| (float
 // bits) of the whole output into *g.amax_out, for a per-tensor quantiser.
@@ -539,4 +596,22 @@ extern "C" int srdit_fp8_quant_apply(const void* x, int64_t M, int64_t K, int64_
     SRDIT_LAUNCH_CHECK("quant_tensor_kernel");
     return SRDIT_OK;
   });
+}
+
+extern "C" int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx,
+                                           void* xq, float* scale, uint32_t* amax_ws,
+                                           void* stream) {
+  if (int rc = check_quant_args("srdit_fp8_quant_tensor_gelu", x, M, K, ldx, xq, scale)) return rc;
+  SRDIT_REQUIRE(amax_ws, "srdit_fp8_quant_tensor_gelu: null amax workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t rows4 = (M + 3) / 4;
+  const unsigned blocks = (unsigned)(rows4 < 4096 ? rows4 : 4096);
+  clear_u32_kernel<<<1, 1, 0, s>>>(amax_ws);
+  SRDIT_LAUNCH_CHECK("clear_u32_kernel");
+  gelu_amax_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), M, K, ldx, amax_ws);
+  SRDIT_LAUNCH_CHECK("gelu_amax_kernel");
+  gelu_quant_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), M, K, ldx,
+                                           static_cast<uint8_t*>(xq), scale, amax_ws);
+  SRDIT_LAUNCH_CHECK("gelu_quant_kernel");
+  return SRDIT_OK;
 }

@@ -10,9 +10,12 @@
 // The weight scale is A's scale, the activation scale B's.
 //
 // One handle per device; a descriptor, layouts and the heuristic's first
-// algorithm are kept per (device, M, N, K, ldo, bias) and reused.  No
-// workspace is given to hipBLASLt, so a call allocates nothing and launches
-// only kernels (it can be captured in a HIP graph).
+// algorithm are kept per (device, M, N, K, ldo, bias, workspace) and reused.
+// Each device also gets one LT_WORKSPACE-byte workspace, allocated by the
+// first call made outside stream capture and kept until the process ends; a
+// call made while its stream is being captured before that uses the plans
+// that need no workspace.  After set-up a call allocates nothing and launches
+// only kernels, so it can be captured in a HIP graph.
 #include "common.h"
 
 #include <hipblaslt/hipblaslt.h>
@@ -32,10 +35,13 @@ struct LtPlan {
   bool ok = false;
 };
 
+constexpr uint64_t LT_WORKSPACE = 64ull << 20;
+
 struct LtState {
   std::mutex mu;
   std::map<int, hipblasLtHandle_t> handles;
-  std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, bool>, LtPlan> plans;
+  std::map<int, void*> workspace;  // per device, nullptr until allocated
+  std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, bool, bool>, LtPlan> plans;
 };
 
 LtState& lt_state() {
@@ -46,7 +52,7 @@ LtState& lt_state() {
 bool lt_ok(hipblasStatus_t st) { return st == HIPBLAS_STATUS_SUCCESS; }
 
 bool make_plan(hipblasLtHandle_t h, LtPlan& p, int64_t M, int64_t N, int64_t K, int64_t ldo,
-               bool bias) {
+               bool bias, uint64_t ws) {
   if (!lt_ok(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F))) return false;
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
   if (!lt_ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta))) ||
@@ -67,7 +73,6 @@ bool make_plan(hipblasLtHandle_t h, LtPlan& p, int64_t M, int64_t N, int64_t K, 
     return false;
   hipblasLtMatmulPreference_t pref = nullptr;
   if (!lt_ok(hipblasLtMatmulPreferenceCreate(&pref))) return false;
-  const uint64_t ws = 0;
   hipblasLtMatmulHeuristicResult_t res{};
   int count = 0;
   const bool got =
@@ -75,7 +80,7 @@ bool make_plan(hipblasLtHandle_t h, LtPlan& p, int64_t M, int64_t N, int64_t K, 
                                                   &ws, sizeof(ws))) &&
       lt_ok(hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.ld, p.ld, pref, 1, &res,
                                             &count)) &&
-      count > 0 && lt_ok(res.state) && res.workspaceSize == 0;
+      count > 0 && lt_ok(res.state) && res.workspaceSize <= ws;
   hipblasLtMatmulPreferenceDestroy(pref);
   if (!got) return false;
   p.algo = res.algo;
@@ -100,11 +105,21 @@ int lt_fp8_gemm(const void* a, const void* b, const float* sa, const float* sb, 
   }
   hipblasLtHandle_t h = hit->second;
   if (!h) return 2;
-  const auto key = std::make_tuple(dev, M, N, K, ldo, bias != nullptr);
+  void*& wsp = st.workspace[dev];
+  if (!wsp) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone &&
+        hipMalloc(&wsp, LT_WORKSPACE) != hipSuccess) {
+      wsp = nullptr;
+      (void)hipGetLastError();
+    }
+  }
+  const bool use_ws = wsp != nullptr;
+  const auto key = std::make_tuple(dev, M, N, K, ldo, bias != nullptr, use_ws);
   auto pit = st.plans.find(key);
   if (pit == st.plans.end()) {
     LtPlan p;
-    p.ok = make_plan(h, p, M, N, K, ldo, bias != nullptr);
+    p.ok = make_plan(h, p, M, N, K, ldo, bias != nullptr, use_ws ? LT_WORKSPACE : 0);
     pit = st.plans.emplace(key, p).first;
   }
   LtPlan& p = pit->second;
@@ -120,8 +135,9 @@ int lt_fp8_gemm(const void* a, const void* b, const float* sa, const float* sb, 
                                                      &bias, sizeof(bias))))
     return 5;
   const float alpha = 1.0f, beta = 0.0f;
-  const hipblasStatus_t rs = hipblasLtMatmul(h, p.desc, &alpha, b, p.la, a, p.lb, &beta, out, p.ld,
-                                             out, p.ld, &p.algo, nullptr, 0, stream);
+  const hipblasStatus_t rs =
+      hipblasLtMatmul(h, p.desc, &alpha, b, p.la, a, p.lb, &beta, out, p.ld, out, p.ld, &p.algo,
+                      use_ws ? wsp : nullptr, use_ws ? LT_WORKSPACE : 0, stream);
   return lt_ok(rs) ? 0 : 6;
 }
 

@@ -37,6 +37,8 @@ SIGNATURES = {
                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p]),
     "srdit_fp8_quant_apply": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
                                        _c_p]),
+    "srdit_fp8_quant_tensor_gelu": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
+                                             _c_p]),
     "srdit_ln_modulate": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_f,
                                    _c_p, _c_i64, _c_p, _c_p]),
     "srdit_residual_gate": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_int, _c_i64, _c_i64, _c_p,
@@ -187,6 +189,16 @@ def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None, force_mfm
                                   int(epilogue) | (GEMM_MFMA if force_mfma else 0),
                                   _ptr(amax_out), _stream(a.device))
     _check(rc, "srdit_fp8_gemm_ex")
+
+
+def fp8_quant_tensor_gelu(x, xq, scale, amax_ws):
+    """Per-tensor e4m3 quantisation of bf16(gelu_tanh(x)) without storing it."""
+    M, K, ldx, dt = _quant_args(x, xq)
+    if dt != 0:
+        raise ValueError("fp8_quant_tensor_gelu: x must be bf16")
+    rc = load().srdit_fp8_quant_tensor_gelu(_ptr(x), M, K, ldx, _ptr(xq), _ptr(scale),
+                                            _ptr(amax_ws), _stream(x.device))
+    _check(rc, "srdit_fp8_quant_tensor_gelu")
 
 
 def fp8_quant_apply(x, xq, scale, amax_ws):

@@ -264,9 +264,11 @@ class Block(nn.Module):
         the gated residuals are one kernel each; the per-tensor fp8 quantiser
         of a Linear's input reuses the amax its producer wrote, and one
         quantised input feeds q, k and v (likewise the text context for the
-        cross-attention k and v); the FFN's GELU and the amax of its output run
-        in the first FFN GEMM's epilogue.  The arithmetic at each point is the
-        reference's (models.py:1304-1351); only reduction orders differ.
+        cross-attention k and v).  The FFN's hidden activation is never
+        stored: the first FFN GEMM writes its bf16 output, and one two-pass
+        quantiser applies the GELU, reduces the amax and writes the e4m3 codes
+        the second GEMM reads.  The arithmetic at each point is the reference's
+        (models.py:1304-1351); only reduction orders differ.
         """
         sa, ca = self.self_attn, self.cross_attn
         cfg = sa.cfg
@@ -321,8 +323,10 @@ class Block(nn.Module):
         ffn_in = torch.empty_like(x)
         _lib.ln_modulate(x2, None, None, mod[4], mod[3], self.norm2.eps, ffn_in, a0)
         xq, xs = quant_from(ffn_in, a0)
-        hmid = self.ffn[0].gemm(xq, xs, epilogue=1, amax_out=a1)
-        hq, hs = quant_from(hmid, a1)
+        hlin = self.ffn[0].gemm(xq, xs)
+        hq = torch.empty(hlin.shape, dtype=FP8_DTYPE, device=dev)
+        hs = torch.empty(1, dtype=torch.float32, device=dev)
+        _lib.fp8_quant_tensor_gelu(hlin, hq, hs, a1)     # GELU, amax and quantisation, h not stored
         y2 = self.ffn[2].gemm(hq, hs)
         x3 = torch.empty_like(x)
         _lib.residual_gate(x2, y2, mod[5], x3)

@@ -285,3 +285,24 @@ def test_fused_block_matches_unfused():
     print(f"[metrics] fused vs op-by-op: max {err.max().item():.3e} mean {err.mean().item():.3e}",
           flush=True)
     assert err.mean().item() <= 2e-3 * plain.float().abs().mean().item()
+
+
+def test_gelu_quantiser_matches_stored_gelu_then_quantiser():
+    """srdit_fp8_quant_tensor_gelu == per-tensor quantiser of a stored
+    bf16(gelu_tanh(x)) from torch, codes and scale bit for bit."""
+    from sr_dit import _lib
+    g = torch.Generator("cpu").manual_seed(12)
+    for M, K in ((300, 384), (2048, 14336)):
+        x = (torch.randn(M, K, generator=g) * 3).to(torch.bfloat16).to(DEV)
+        h = F.gelu(x.float(), approximate="tanh").to(torch.bfloat16)
+        want_q = torch.empty(M, K, dtype=F8, device=DEV)
+        want_s = torch.empty(1, dtype=torch.float32, device=DEV)
+        ws = torch.zeros(1, dtype=torch.int32, device=DEV)
+        _lib.fp8_quant_tensor(h, want_q, want_s, ws)
+        got_q = torch.empty_like(want_q)
+        got_s = torch.empty_like(want_s)
+        ws2 = torch.zeros(1, dtype=torch.int32, device=DEV)
+        _lib.fp8_quant_tensor_gelu(x, got_q, got_s, ws2)
+        torch.cuda.synchronize()
+        assert torch.equal(got_s, want_s), (got_s.item(), want_s.item())
+        assert torch.equal(got_q.view(torch.uint8), want_q.view(torch.uint8))
