@@ -226,11 +226,11 @@ __device__ __forceinline__ float bf16_rt(float x) {
 }
 
 // The FFN's hidden activation h = bf16(gelu_tanh(x)) for x [M, K] bf16 (the
-// first Linear's bf16 output), quantised per tensor without storing h: pass 1
-// reduces max |h| into amax_ws, pass 2 recomputes h and writes its e4m3 codes
-// and the scale, exactly as the per-tensor quantiser of a stored h would.
-__global__ __launch_bounds__(256) void gelu_amax_kernel(const uint16_t* __restrict__ x, int64_t M,
-                                                        int64_t K, int64_t ldx,
+// first Linear's bf16 output), then its per-tensor quantisation: pass 1 writes
+// h (in place over x when h == x) and reduces max |h| into amax_ws; pass 2 is
+// the per-tensor quantiser of h.  GELU is evaluated once per element.
+__global__ __launch_bounds__(256) void gelu_amax_kernel(const uint16_t* x, int64_t M, int64_t K,
+                                                        int64_t ldx, uint16_t* h, int64_t ldh,
                                                         uint32_t* __restrict__ amax_ws) {
   __shared__ uint32_t part[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -238,11 +238,22 @@ __global__ __launch_bounds__(256) void gelu_amax_kernel(const uint16_t* __restri
   uint32_t amax = 0;
   for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
     const uint16_t* xr = x + row * ldx;
+    uint4* hr = reinterpret_cast<uint4*>(h + row * ldh);
     for (int64_t c = lane; c < nchunk; c += 64) {
       float f[8];
       Load8<uint16_t>::get(xr, c, f);
+      uint32_t w[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) f[i] = bf16_rt(gelu_tanh(f[i]));
+      for (int i = 0; i < 4; ++i) {
+        typedef float f32x2v __attribute__((ext_vector_type(2)));
+        typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+        w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                                f32x2v{gelu_tanh(f[2 * i]), gelu_tanh(f[2 * i + 1])},
+                                                bf16x2v));
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+      hr[c] = make_uint4(w[0], w[1], w[2], w[3]);
       amax = abs_bits_max8(f, amax);
     }
   }
@@ -250,28 +261,6 @@ __global__ __launch_bounds__(256) void gelu_amax_kernel(const uint16_t* __restri
   if (lane == 0) part[wave] = amax;
   __syncthreads();
   if (threadIdx.x == 0) atomicMax(amax_ws, max(max(part[0], part[1]), max(part[2], part[3])));
-}
-
-__global__ __launch_bounds__(256) void gelu_quant_kernel(const uint16_t* __restrict__ x, int64_t M,
-                                                         int64_t K, int64_t ldx,
-                                                         uint8_t* __restrict__ xq,
-                                                         float* __restrict__ scale,
-                                                         const uint32_t* __restrict__ amax_ws) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const float s = scale_from_amax_bits(*amax_ws);
-  if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
-  const int64_t nchunk = K >> 3;
-  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
-    const uint16_t* xr = x + row * ldx;
-    uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
-    for (int64_t c = lane; c < nchunk; c += 64) {
-      float f[8];
-      Load8<uint16_t>::get(xr, c, f);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) f[i] = bf16_rt(gelu_tanh(f[i]));
-      qr[c] = to_e4m3x8(f, s);
-    }
-  }
 }
 
 // EPI 0: out = bf16(v); EPI 1: out = bf16(gelu(bf16(v))), the Linear's bf16
@@ -599,19 +588,23 @@ extern "C" int srdit_fp8_quant_apply(const void* x, int64_t M, int64_t K, int64_
 }
 
 extern "C" int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx,
-                                           void* xq, float* scale, uint32_t* amax_ws,
-                                           void* stream) {
+                                           void* h, int64_t ldh, void* xq, float* scale,
+                                           uint32_t* amax_ws, void* stream) {
   if (int rc = check_quant_args("srdit_fp8_quant_tensor_gelu", x, M, K, ldx, xq, scale)) return rc;
-  SRDIT_REQUIRE(amax_ws, "srdit_fp8_quant_tensor_gelu: null amax workspace");
+  SRDIT_REQUIRE(amax_ws && h, "srdit_fp8_quant_tensor_gelu: null amax workspace or h");
+  SRDIT_REQUIRE(aligned16(h) && ldh >= K && ldh % 8 == 0 && (h == x ? ldh == ldx : true),
+                "srdit_fp8_quant_tensor_gelu: h must be 16-byte aligned with ldh >= K, ldh %% 8 == 0 "
+                "(ldh == ldx in place)");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t rows4 = (M + 3) / 4;
   const unsigned blocks = (unsigned)(rows4 < 4096 ? rows4 : 4096);
   clear_u32_kernel<<<1, 1, 0, s>>>(amax_ws);
   SRDIT_LAUNCH_CHECK("clear_u32_kernel");
-  gelu_amax_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), M, K, ldx, amax_ws);
+  gelu_amax_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), M, K, ldx,
+                                          static_cast<uint16_t*>(h), ldh, amax_ws);
   SRDIT_LAUNCH_CHECK("gelu_amax_kernel");
-  gelu_quant_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), M, K, ldx,
-                                           static_cast<uint8_t*>(xq), scale, amax_ws);
-  SRDIT_LAUNCH_CHECK("gelu_quant_kernel");
+  quant_tensor_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(h), M, K, ldh,
+                                                       static_cast<uint8_t*>(xq), scale, amax_ws);
+  SRDIT_LAUNCH_CHECK("quant_tensor_kernel");
   return SRDIT_OK;
 }

@@ -37,8 +37,8 @@ SIGNATURES = {
                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p]),
     "srdit_fp8_quant_apply": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
                                        _c_p]),
-    "srdit_fp8_quant_tensor_gelu": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
-                                             _c_p]),
+    "srdit_fp8_quant_tensor_gelu": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
+                                             _c_p, _c_p, _c_p]),
     "srdit_ln_modulate": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_f,
                                    _c_p, _c_i64, _c_p, _c_p]),
     "srdit_residual_gate": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_int, _c_i64, _c_i64, _c_p,
@@ -191,13 +191,17 @@ def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None, force_mfm
     _check(rc, "srdit_fp8_gemm_ex")
 
 
-def fp8_quant_tensor_gelu(x, xq, scale, amax_ws):
-    """Per-tensor e4m3 quantisation of bf16(gelu_tanh(x)) without storing it."""
+def fp8_quant_tensor_gelu(x, xq, scale, amax_ws, h=None):
+    """h = bf16(gelu_tanh(x)) (into x itself when h is None), then the per-tensor
+    e4m3 quantisation of h into xq / scale."""
     M, K, ldx, dt = _quant_args(x, xq)
     if dt != 0:
         raise ValueError("fp8_quant_tensor_gelu: x must be bf16")
-    rc = load().srdit_fp8_quant_tensor_gelu(_ptr(x), M, K, ldx, _ptr(xq), _ptr(scale),
-                                            _ptr(amax_ws), _stream(x.device))
+    h = x if h is None else h
+    if h.dtype != torch.bfloat16 or tuple(h.shape) != (M, K) or h.stride(1) != 1:
+        raise ValueError("fp8_quant_tensor_gelu: h must be bf16 shaped like x with unit column stride")
+    rc = load().srdit_fp8_quant_tensor_gelu(_ptr(x), M, K, ldx, _ptr(h), h.stride(0), _ptr(xq),
+                                            _ptr(scale), _ptr(amax_ws), _stream(x.device))
     _check(rc, "srdit_fp8_quant_tensor_gelu")
 
 

@@ -264,10 +264,9 @@ class Block(nn.Module):
         the gated residuals are one kernel each; the per-tensor fp8 quantiser
         of a Linear's input reuses the amax its producer wrote, and one
         quantised input feeds q, k and v (likewise the text context for the
-        cross-attention k and v).  The FFN's hidden activation is never
-        stored: the first FFN GEMM writes its bf16 output, and one two-pass
-        quantiser applies the GELU, reduces the amax and writes the e4m3 codes
-        the second GEMM reads.  The arithmetic at each point is the reference's
+        cross-attention k and v).  The FFN's first GEMM writes its bf16
+        output; one call then applies the GELU in place (once per element),
+        reduces the amax and writes the e4m3 codes the second GEMM reads.  The arithmetic at each point is the reference's
         (models.py:1304-1351); only reduction orders differ.
         """
         sa, ca = self.self_attn, self.cross_attn
@@ -326,7 +325,7 @@ class Block(nn.Module):
         hlin = self.ffn[0].gemm(xq, xs)
         hq = torch.empty(hlin.shape, dtype=FP8_DTYPE, device=dev)
         hs = torch.empty(1, dtype=torch.float32, device=dev)
-        _lib.fp8_quant_tensor_gelu(hlin, hq, hs, a1)     # GELU, amax and quantisation, h not stored
+        _lib.fp8_quant_tensor_gelu(hlin, hq, hs, a1)     # h = GELU in place, amax, quantisation
         y2 = self.ffn[2].gemm(hq, hs)
         x3 = torch.empty_like(x)
         _lib.residual_gate(x2, y2, mod[5], x3)

@@ -288,8 +288,9 @@ def test_fused_block_matches_unfused():
 
 
 def test_gelu_quantiser_matches_stored_gelu_then_quantiser():
-    """srdit_fp8_quant_tensor_gelu == per-tensor quantiser of a stored
-    bf16(gelu_tanh(x)) from torch, codes and scale bit for bit."""
+    """srdit_fp8_quant_tensor_gelu: h == torch's bf16(gelu_tanh(x)) and the codes
+    and scale == the per-tensor quantiser of that h, bit for bit, into a separate
+    buffer and in place."""
     from sr_dit import _lib
     g = torch.Generator("cpu").manual_seed(12)
     for M, K in ((300, 384), (2048, 14336)):
@@ -302,7 +303,14 @@ def test_gelu_quantiser_matches_stored_gelu_then_quantiser():
         got_q = torch.empty_like(want_q)
         got_s = torch.empty_like(want_s)
         ws2 = torch.zeros(1, dtype=torch.int32, device=DEV)
-        _lib.fp8_quant_tensor_gelu(x, got_q, got_s, ws2)
+        hbuf = torch.empty_like(x)
+        _lib.fp8_quant_tensor_gelu(x, got_q, got_s, ws2, h=hbuf)       # separate h
         torch.cuda.synchronize()
+        assert torch.equal(hbuf, h)
         assert torch.equal(got_s, want_s), (got_s.item(), want_s.item())
+        assert torch.equal(got_q.view(torch.uint8), want_q.view(torch.uint8))
+        xi = x.clone()
+        _lib.fp8_quant_tensor_gelu(xi, got_q, got_s, ws2)               # in place
+        torch.cuda.synchronize()
+        assert torch.equal(xi, h)
         assert torch.equal(got_q.view(torch.uint8), want_q.view(torch.uint8))
