@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-step", action="store_true",
                     help="skip the SR-DiT refiner step (30 blocks, hipGraph) measurement")
+    ap.add_argument("--no-prod", action="store_true",
+                    help="skip the shipped-geometry (4x4 blocks, radius 3) window timings")
     ap.add_argument("--step-iters", type=int, default=5,
                     help="timed graph replays of the refiner step")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
@@ -203,6 +205,60 @@ def refiner_step(steps, warmup, layers=30):
             "data": "synthetic: N(0,0.02) weights, N(0,1) activations and context"}
 
 
+def production_window(steps, warmup=3):
+    """The refiner's shipped window geometry: 4x4-token blocks, radius 3, one 3-frame
+    query chunk of 45x80 against 12 KV frames (streaming rule), without an anchor and
+    with the LQ anchor in its "frame" and "chunk" alignments (one 45x80 anchor frame per
+    query frame).  Useful TFLOP/s per kernel launch; the single-window kernel runs all
+    three (48-query windows give the grouped kernel nothing to pair)."""
+    import torch
+    from sr_dit import attention as att
+    from sr_dit import blockgrid_hip as bgh
+    from sr_dit import workloads as wl
+
+    dev = torch.device("cuda:0")
+    f_cur, f_kv, h, w = 3, 12, 45, 80
+    spec = att._BlockGridSpec(f_cur=f_cur, f_kv=f_kv, h=h, w=w, block_t=3, bh=4, bw=4, rh=3,
+                              rw=3, rt=3, streaming=True)
+    n, d = wl.N_HEADS, wl.HEAD_DIM
+    L = h * w
+    g = torch.Generator("cpu").manual_seed(0)
+    sc = d ** -0.5
+    # KV tensor = f_cur anchor frames, then the 12 HR frames (the kernel reads the
+    # anchor prefix only in the anchor modes)
+    q = (torch.randn(f_cur * L, n, d, generator=g) * sc).to(torch.bfloat16).to(dev)
+    k = (torch.randn((f_cur + f_kv) * L, n, d, generator=g) * sc).to(torch.bfloat16).to(dev)
+    v = (torch.randn((f_cur + f_kv) * L, n, d, generator=g) * sc).to(torch.bfloat16).to(dev)
+    out = torch.empty_like(q)
+    res = {"workload": "window attention 3x45x80 query chunk vs 12 KV frames, 24 heads x 128, "
+                       "4x4 blocks, radius 3 (7x7 blocks), streaming rule; anchor: one 45x80 LQ "
+                       "frame per query frame",
+           "steps": steps}
+    stream = torch.cuda.current_stream(dev)
+    for mode in (None, "frame", "chunk"):
+        plan = bgh.build_plan(spec, anchor_mode=mode)
+
+        def run():
+            bgh.run_blockgrid_hip(q, k, v, out, plan=plan, f_cur=f_cur, h=h, w=w, n=n, d=d,
+                                  anchor_mode=mode)
+
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        flops = wl.plan_useful_flops(plan)
+        res[mode or "no_anchor"] = {"us": round(ms * 1e3, 1), "useful_gflop": round(flops / 1e9, 1),
+                                    "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+    return res
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -278,6 +334,8 @@ def main():
                      "algorithmic_hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1)},
         "wall_s_timed_region": round(wall, 4),
     }
+    if not args.no_prod:
+        result["production_window"] = production_window(20)
     if not args.no_step:
         result["refiner_step"] = refiner_step(args.step_iters, 1)
     if not args.no_cpu_baseline:

@@ -46,6 +46,8 @@ struct WinArgs {
   int64_t q_tokens, kv_tokens;
   int n_heads;
   float scale_log2;  // softmax scale * log2(e)
+  int ring_R, ring_nc;       // in-place KV cache layout (ring_R == 0: plain)
+  const int32_t* ring_head;  // device int32: ring slot of the oldest cached frame
 };
 
 constexpr int WAVES = 2;  // wavefronts per workgroup, 32 queries each
@@ -67,10 +69,12 @@ struct Tile {
 };
 
 // Token of key j of a run, walked forward KN keys per step: the lane keeps its
-// key's index within the current frame and that frame's first token.
+// key's index within the current frame, the frame's logical index and that
+// frame's first token (the ring maps logical frames to physical ones).
 struct KeyCursor {
   int rr;         // index of the key within its frame of the run
-  int frame_tok;  // token of that frame's first cuboid cell: base + (t0+t)*frame_len
+  int f;          // logical frame: t0 + t
+  int frame_tok;  // token of that frame's first cuboid cell: base + phys(f) * frame_len
 };
 
 __device__ __forceinline__ KeyCursor cursor_at(const KeyRun& k, int j) {
@@ -78,7 +82,8 @@ __device__ __forceinline__ KeyCursor cursor_at(const KeyRun& k, int j) {
   const int t = fdiv(j, sp, k.r_sp);
   KeyCursor c;
   c.rr = j - t * sp;
-  c.frame_tok = k.base + (k.t0 + t) * k.frame_len;
+  c.f = k.t0 + t;
+  c.frame_tok = k.base + ring_frame(k.ring, c.f) * k.frame_len;
   return c;
 }
 
@@ -91,10 +96,13 @@ __device__ __forceinline__ int cursor_token(const KeyRun& k, const KeyCursor& c)
 __device__ __forceinline__ void cursor_advance(const KeyRun& k, KeyCursor& c, int by) {
   const int sp = k.rows * k.cols;
   c.rr += by;
+  bool moved = false;
   while (c.rr >= sp) {  // at most ceil(by / sp) frames
     c.rr -= sp;
-    c.frame_tok += k.frame_len;
+    ++c.f;
+    moved = true;
   }
+  if (moved) c.frame_tok = k.base + ring_frame(k.ring, c.f) * k.frame_len;
 }
 
 // Walk one key run with the online softmax.  `seg` >= 0 restricts the run to
@@ -323,6 +331,7 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
 
   const int sp_hr = kh_l * kw_l;
   const int sp_a = kh_l_a * kw_l_a;
+  const KvRing ring = load_ring(a.ring_R, a.ring_nc, a.ring_head);
   const bool anchor_ok = kh_l_a > 0 && kw_l_a > 0 && h_a > 0 && w_a > 0;
   if (MODE == 0) {
     // anchor prefix (a_frames whole-chunk anchor frames), then the HR cuboid
@@ -332,7 +341,7 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
                        ksh, vsh, lo);
     }
     if (sp_hr > 0 && kv_tl > 0) {
-      KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
+      KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W, ring);
       attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kvrsrc, kv_tokens, a.scale_log2,
                        ksh, vsh, lo);
     }
@@ -350,7 +359,7 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
       }
     }
     if (sp_hr > 0 && kv_tl > 0) {
-      KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W);
+      KeyRun hr = make_run(kv_tl * sp_hr, a.hr_base, L, kv_t0, kh0, kw0, kh_l, kw_l, a.W, ring);
       attend_run<T, D>(st, hr, -1, wave, qframe, qvalid, kvrsrc, kv_tokens, a.scale_log2,
                        ksh, vsh, lo);
     }
@@ -386,45 +395,47 @@ int launch_window(const WinArgs& a, int mode, uint32_t grid, hipStream_t stream)
 }  // namespace
 }  // namespace srdit
 
-extern "C" int srdit_window_attn_fwd(const void* q, const void* k, const void* v, void* o,
-                                     const int32_t* params, const int32_t* order, int n_w,
-                                     int m_tiles, int p_stride, int hr_base, int H, int W,
-                                     int64_t q_tokens, int64_t kv_tokens, int n_heads,
-                                     int head_dim, float scale, int mode, int dtype,
-                                     void* stream) {
-  using namespace srdit;
-  SRDIT_REQUIRE(q && k && v && o && params && order, "srdit_window_attn_fwd: null pointer");
+namespace srdit {
+namespace {
+
+int window_entry(const char* fn, const void* q, const void* k, const void* v, void* o,
+                 const int32_t* params, const int32_t* order, int n_w, int m_tiles, int p_stride,
+                 int hr_base, int H, int W, int64_t q_tokens, int64_t kv_tokens, int n_heads,
+                 int head_dim, float scale, int mode, int ring_R, int ring_nc,
+                 const int32_t* ring_head, int dtype, void* stream) {
+  SRDIT_REQUIRE(q && k && v && o && params && order, "%s: null pointer", fn);
   SRDIT_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
-                "srdit_window_attn_fwd: q/k/v/o must be 16-byte aligned");
-  SRDIT_REQUIRE(mode == 0 || mode == 1, "srdit_window_attn_fwd: mode must be 0 or 1, got %d", mode);
+                "%s: q/k/v/o must be 16-byte aligned", fn);
+  SRDIT_REQUIRE(mode == 0 || mode == 1, "%s: mode must be 0 or 1, got %d", fn, mode);
   SRDIT_REQUIRE(p_stride == (mode == 0 ? 19 : 17),
-                "srdit_window_attn_fwd: p_stride %d does not match mode %d", p_stride, mode);
+                "%s: p_stride %d does not match mode %d", fn, p_stride, mode);
   SRDIT_REQUIRE(n_w >= 1 && m_tiles >= 1 && n_heads >= 1 && H >= 1 && W >= 1 && hr_base >= 0,
-                "srdit_window_attn_fwd: bad sizes (n_w=%d m_tiles=%d n_heads=%d H=%d W=%d hr_base=%d)",
+                "%s: bad sizes (n_w=%d m_tiles=%d n_heads=%d H=%d W=%d hr_base=%d)", fn,
                 n_w, m_tiles, n_heads, H, W, hr_base);
   SRDIT_REQUIRE(q_tokens >= 1 && kv_tokens >= 1 && q_tokens < (1LL << 31) && kv_tokens < (1LL << 31),
-                "srdit_window_attn_fwd: token counts out of range");
-  SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 22), "srdit_window_attn_fwd: grid too large");
+                "%s: token counts out of range", fn);
+  SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 22), "%s: grid too large", fn);
   SRDIT_REQUIRE(kv_tokens * n_heads * head_dim * 2 < (1LL << 31) && q_tokens < (1LL << 24),
-                "srdit_window_attn_fwd: K/V must span fewer than 2^31 bytes and 2^24 tokens");
+                "%s: K/V must span fewer than 2^31 bytes and 2^24 tokens", fn);
   SRDIT_REQUIRE(static_cast<int64_t>(n_heads) * head_dim * 2 < (1LL << 14),
-                "srdit_window_attn_fwd: token stride n_heads*head_dim*2 must be below 16384 bytes "
-                "(structured-buffer stride)");
+                "%s: token stride n_heads*head_dim*2 must be below 16384 bytes "
+                "(structured-buffer stride)", fn);
   if (head_dim != 64 && head_dim != 128) {
-    set_error("srdit_window_attn_fwd: head_dim %d unsupported (64 or 128)", head_dim);
+    set_error("%s: head_dim %d unsupported (64 or 128)", fn, head_dim);
     return SRDIT_EUNSUPPORTED;
   }
   if (dtype != SRDIT_DTYPE_BF16 && dtype != SRDIT_DTYPE_FP16) {
-    set_error("srdit_window_attn_fwd: dtype code %d unsupported", dtype);
+    set_error("%s: dtype code %d unsupported", fn, dtype);
     return SRDIT_EUNSUPPORTED;
   }
   const int64_t grid64 = static_cast<int64_t>(n_w) * m_tiles * n_heads;
-  SRDIT_REQUIRE(grid64 < (1LL << 31), "srdit_window_attn_fwd: too many tasks");
+  SRDIT_REQUIRE(grid64 < (1LL << 31), "%s: too many tasks", fn);
   WinArgs a;
   a.q = q; a.k = k; a.v = v; a.o = o; a.params = params; a.order = order;
   a.n_w = n_w; a.m_tiles = m_tiles; a.p_stride = p_stride; a.hr_base = hr_base; a.H = H; a.W = W;
   a.q_tokens = q_tokens; a.kv_tokens = kv_tokens; a.n_heads = n_heads;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.ring_R = ring_R; a.ring_nc = ring_nc; a.ring_head = ring_head;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint32_t grid = static_cast<uint32_t>(grid64);
   if (dtype == SRDIT_DTYPE_BF16)
@@ -432,4 +443,39 @@ extern "C" int srdit_window_attn_fwd(const void* q, const void* k, const void* v
                            : launch_window<__bf16, 64>(a, mode, grid, s);
   return head_dim == 128 ? launch_window<_Float16, 128>(a, mode, grid, s)
                          : launch_window<_Float16, 64>(a, mode, grid, s);
+}
+
+}  // namespace
+}  // namespace srdit
+
+extern "C" int srdit_window_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                                     const int32_t* params, const int32_t* order, int n_w,
+                                     int m_tiles, int p_stride, int hr_base, int H, int W,
+                                     int64_t q_tokens, int64_t kv_tokens, int n_heads,
+                                     int head_dim, float scale, int mode, int dtype,
+                                     void* stream) {
+  return srdit::window_entry("srdit_window_attn_fwd", q, k, v, o, params, order, n_w, m_tiles,
+                             p_stride, hr_base, H, W, q_tokens, kv_tokens, n_heads, head_dim,
+                             scale, mode, 0, 0, nullptr, dtype, stream);
+}
+
+extern "C" int srdit_window_attn_ring_fwd(const void* q, const void* k, const void* v, void* o,
+                                          const int32_t* params, const int32_t* order, int n_w,
+                                          int m_tiles, int p_stride, int hr_base, int H, int W,
+                                          int64_t q_tokens, int64_t kv_tokens, int n_heads,
+                                          int head_dim, float scale, int mode, int ring_frames,
+                                          int ring_cached, const int32_t* ring_head, int dtype,
+                                          void* stream) {
+  using namespace srdit;
+  SRDIT_REQUIRE(ring_head != nullptr, "srdit_window_attn_ring_fwd: null ring_head");
+  SRDIT_REQUIRE(ring_frames >= 1 && ring_cached >= 0 && ring_cached <= ring_frames,
+                "srdit_window_attn_ring_fwd: need 1 <= ring_frames and 0 <= ring_cached <= "
+                "ring_frames (got %d, %d)", ring_frames, ring_cached);
+  SRDIT_REQUIRE(hr_base >= 0 && static_cast<int64_t>(hr_base) +
+                    static_cast<int64_t>(ring_frames) * H * W <= kv_tokens,
+                "srdit_window_attn_ring_fwd: kv_tokens %lld do not cover the anchor prefix and "
+                "%d ring frames", static_cast<long long>(kv_tokens), ring_frames);
+  return window_entry("srdit_window_attn_ring_fwd", q, k, v, o, params, order, n_w, m_tiles,
+                      p_stride, hr_base, H, W, q_tokens, kv_tokens, n_heads, head_dim, scale,
+                      mode, ring_frames, ring_cached, ring_head, dtype, stream);
 }

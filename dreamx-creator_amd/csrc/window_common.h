@@ -197,6 +197,34 @@ __device__ __forceinline__ LaneOff<D> make_lane_offsets(int wave) {
 //   token = base + (t0 + j/sp)*frame_len + (r0 + (j%sp)/cols)*Wg + c0 + (j%sp)%cols
 // The HR cuboid, the anchor prefix of the plain kernel and an anchor segment of
 // the frame kernel are all this formula with their own grid.
+// Frame layout of a streaming KV cache kept in place: R ring slots holding the
+// nc cached frames (oldest first, cached frame f in slot (head + f) mod R),
+// followed by the current chunk's frames (logical frame nc + i at R + i).
+// R == 0 is the plain layout, logical frame f at f.
+struct KvRing {
+  int R, nc, head;  // 0 <= head < R, 0 <= nc <= R
+};
+
+__device__ __forceinline__ int ring_frame(const KvRing& r, int f) {
+  if (r.R <= 0) return f;
+  if (f < r.nc) {
+    const int s = r.head + f;  // < 2R
+    return s >= r.R ? s - r.R : s;
+  }
+  return r.R + (f - r.nc);
+}
+
+// The ring of a launch: R and nc by value, head from device memory (so one
+// captured launch stays valid while the ring advances), clamped into range.
+__device__ __forceinline__ KvRing load_ring(int R, int nc, const int32_t* head) {
+  KvRing r;
+  r.R = R > 0 ? R : 0;
+  r.nc = nc < 0 ? 0 : (nc > r.R ? r.R : nc);
+  int h = (r.R > 0 && head != nullptr) ? __builtin_amdgcn_readfirstlane(head[0]) : 0;
+  r.head = (h < 0 || h >= r.R) ? 0 : h;
+  return r;
+}
+
 struct KeyRun {
   int n;          // keys in the run
   int base;       // token offset of frame 0 of the run
@@ -205,28 +233,20 @@ struct KeyRun {
   int rows, cols; // cuboid rows / columns per frame
   int Wg;         // grid width (row stride in tokens)
   float r_sp, r_cols;
+  KvRing ring;    // logical -> physical frame (R == 0: identity)
 };
 
 __device__ __forceinline__ KeyRun make_run(int n, int base, int frame_len, int t0, int r0,
-                                           int c0, int rows, int cols, int Wg) {
+                                           int c0, int rows, int cols, int Wg,
+                                           KvRing ring = KvRing{0, 0, 0}) {
   KeyRun k;
   k.n = n; k.base = base; k.frame_len = frame_len; k.t0 = t0; k.r0 = r0; k.c0 = c0;
   k.rows = rows; k.cols = cols; k.Wg = Wg;
   k.r_sp = 1.0f / static_cast<float>(rows * cols);
   k.r_cols = 1.0f / static_cast<float>(cols);
+  k.ring = ring;
   return k;
 }
-
-// Token index of key j of the run (token counts are below 2^31, checked on entry).
-__device__ __forceinline__ int run_token(const KeyRun& k, int j) {
-  const int sp = k.rows * k.cols;
-  const int t = fdiv(j, sp, k.r_sp);
-  const int rr = j - t * sp;
-  const int row = fdiv(rr, k.cols, k.r_cols);
-  const int col = rr - row * k.cols;
-  return k.base + (k.t0 + t) * k.frame_len + (k.r0 + row) * k.Wg + (k.c0 + col);
-}
-
 
 }  // namespace win
 }  // namespace srdit

@@ -42,6 +42,8 @@ struct GroupArgs {
   int64_t q_tokens, kv_tokens;
   int n_heads;
   float scale_log2;  // softmax scale * log2(e)
+  int ring_R, ring_nc;       // in-place KV cache layout (ring_R == 0: plain)
+  const int32_t* ring_head;  // device int32: ring slot of the oldest cached frame
 };
 
 constexpr int GKN = 32;  // keys per block
@@ -237,9 +239,10 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   const int col_start = src_key - row_start * kwl;
   const int last_tok = (kh_l - 1) * a.W + (kw_l - 1);  // last key of the extent, frame-relative
   const int frame0_tok = a.hr_base + kh0 * a.W + kw0;
+  const KvRing ring = load_ring(a.ring_R, a.ring_nc, a.ring_head);
   auto fbase_of = [&](int fs_) __attribute__((always_inline)) -> int {
     const int f = frame_of(fs_);
-    return f >= 0 ? frame0_tok + f * L : -1;
+    return f >= 0 ? frame0_tok + ring_frame(ring, f) * L : -1;
   };
   FillCursor cur;
   // Per-slot state of the cursor, refreshed when it enters a frame slot.
@@ -515,46 +518,84 @@ int launch_group(const GroupArgs& a, uint32_t grid, hipStream_t stream) {
 }  // namespace
 }  // namespace srdit
 
-extern "C" int srdit_window_attn_grouped_fwd(const void* q, const void* k, const void* v, void* o,
-                                             const int32_t* params, const int32_t* groups,
-                                             int n_w, int n_groups, int hr_base, int H, int W,
-                                             int64_t q_tokens, int64_t kv_tokens, int n_heads,
-                                             int head_dim, float scale, int dtype, void* stream) {
-  using namespace srdit;
-  SRDIT_REQUIRE(q && k && v && o && params && groups, "srdit_window_attn_grouped_fwd: null pointer");
+namespace srdit {
+namespace {
+
+int group_entry(const char* fn, const void* q, const void* k, const void* v, void* o,
+                const int32_t* params, const int32_t* groups, int n_w, int n_groups, int hr_base,
+                int H, int W, int64_t q_tokens, int64_t kv_tokens, int n_heads, int head_dim,
+                float scale, int ring_R, int ring_nc, const int32_t* ring_head, int dtype,
+                void* stream) {
+  SRDIT_REQUIRE(q && k && v && o && params && groups, "%s: null pointer", fn);
   SRDIT_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
-                "srdit_window_attn_grouped_fwd: q/k/v/o must be 16-byte aligned");
+                "%s: q/k/v/o must be 16-byte aligned", fn);
   SRDIT_REQUIRE(n_w >= 1 && n_groups >= 1 && n_heads >= 1 && H >= 1 && W >= 1 && hr_base >= 0,
-                "srdit_window_attn_grouped_fwd: bad sizes (n_w=%d n_groups=%d n_heads=%d H=%d W=%d "
-                "hr_base=%d)", n_w, n_groups, n_heads, H, W, hr_base);
+                "%s: bad sizes (n_w=%d n_groups=%d n_heads=%d H=%d W=%d "
+                "hr_base=%d)", fn, n_w, n_groups, n_heads, H, W, hr_base);
   SRDIT_REQUIRE(q_tokens >= 1 && kv_tokens >= 1 && q_tokens < (1LL << 24),
-                "srdit_window_attn_grouped_fwd: token counts out of range");
-  SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 22), "srdit_window_attn_grouped_fwd: grid too large");
+                "%s: token counts out of range", fn);
+  SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 22), "%s: grid too large", fn);
   SRDIT_REQUIRE(kv_tokens * n_heads * head_dim * 2 < (1LL << 31),
-                "srdit_window_attn_grouped_fwd: K/V must span fewer than 2^31 bytes");
+                "%s: K/V must span fewer than 2^31 bytes", fn);
   SRDIT_REQUIRE(static_cast<int64_t>(n_heads) * head_dim * 2 < (1LL << 14),
-                "srdit_window_attn_grouped_fwd: token stride n_heads*head_dim*2 must be below 16384 "
-                "bytes (structured-buffer stride)");
+                "%s: token stride n_heads*head_dim*2 must be below 16384 "
+                "bytes (structured-buffer stride)", fn);
   SRDIT_REQUIRE(scale > 0.f && scale < 1e30f,
-                "srdit_window_attn_grouped_fwd: softmax scale must be positive and finite");
+                "%s: softmax scale must be positive and finite", fn);
   if (head_dim != 64 && head_dim != 128) {
-    set_error("srdit_window_attn_grouped_fwd: head_dim %d unsupported (64 or 128)", head_dim);
+    set_error("%s: head_dim %d unsupported (64 or 128)", fn, head_dim);
     return SRDIT_EUNSUPPORTED;
   }
   if (dtype != SRDIT_DTYPE_BF16 && dtype != SRDIT_DTYPE_FP16) {
-    set_error("srdit_window_attn_grouped_fwd: dtype code %d unsupported", dtype);
+    set_error("%s: dtype code %d unsupported", fn, dtype);
     return SRDIT_EUNSUPPORTED;
   }
   const int64_t grid64 = static_cast<int64_t>(n_groups) * n_heads;
-  SRDIT_REQUIRE(grid64 < (1LL << 31), "srdit_window_attn_grouped_fwd: too many tasks");
+  SRDIT_REQUIRE(grid64 < (1LL << 31), "%s: too many tasks", fn);
   GroupArgs a;
   a.q = q; a.k = k; a.v = v; a.o = o; a.params = params; a.groups = groups;
   a.n_w = n_w; a.n_groups = n_groups; a.hr_base = hr_base; a.H = H; a.W = W;
   a.q_tokens = q_tokens; a.kv_tokens = kv_tokens; a.n_heads = n_heads;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.ring_R = ring_R; a.ring_nc = ring_nc; a.ring_head = ring_head;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint32_t grid = static_cast<uint32_t>(grid64);
   if (dtype == SRDIT_DTYPE_BF16)
     return head_dim == 128 ? launch_group<__bf16, 128>(a, grid, s) : launch_group<__bf16, 64>(a, grid, s);
   return head_dim == 128 ? launch_group<_Float16, 128>(a, grid, s) : launch_group<_Float16, 64>(a, grid, s);
+}
+
+}  // namespace
+}  // namespace srdit
+
+extern "C" int srdit_window_attn_grouped_fwd(const void* q, const void* k, const void* v, void* o,
+                                             const int32_t* params, const int32_t* groups,
+                                             int n_w, int n_groups, int hr_base, int H, int W,
+                                             int64_t q_tokens, int64_t kv_tokens, int n_heads,
+                                             int head_dim, float scale, int dtype, void* stream) {
+  return srdit::group_entry("srdit_window_attn_grouped_fwd", q, k, v, o, params, groups, n_w,
+                            n_groups, hr_base, H, W, q_tokens, kv_tokens, n_heads, head_dim,
+                            scale, 0, 0, nullptr, dtype, stream);
+}
+
+extern "C" int srdit_window_attn_grouped_ring_fwd(const void* q, const void* k, const void* v,
+                                                  void* o, const int32_t* params,
+                                                  const int32_t* groups, int n_w, int n_groups,
+                                                  int hr_base, int H, int W, int64_t q_tokens,
+                                                  int64_t kv_tokens, int n_heads, int head_dim,
+                                                  float scale, int ring_frames, int ring_cached,
+                                                  const int32_t* ring_head, int dtype,
+                                                  void* stream) {
+  using namespace srdit;
+  SRDIT_REQUIRE(ring_head != nullptr, "srdit_window_attn_grouped_ring_fwd: null ring_head");
+  SRDIT_REQUIRE(ring_frames >= 1 && ring_cached >= 0 && ring_cached <= ring_frames,
+                "srdit_window_attn_grouped_ring_fwd: need 1 <= ring_frames and 0 <= ring_cached "
+                "<= ring_frames (got %d, %d)", ring_frames, ring_cached);
+  SRDIT_REQUIRE(hr_base >= 0 && static_cast<int64_t>(hr_base) +
+                    static_cast<int64_t>(ring_frames) * H * W <= kv_tokens,
+                "srdit_window_attn_grouped_ring_fwd: kv_tokens %lld do not cover the anchor "
+                "prefix and %d ring frames", static_cast<long long>(kv_tokens), ring_frames);
+  return group_entry("srdit_window_attn_grouped_ring_fwd", q, k, v, o, params, groups, n_w,
+                     n_groups, hr_base, H, W, q_tokens, kv_tokens, n_heads, head_dim, scale,
+                     ring_frames, ring_cached, ring_head, dtype, stream);
 }

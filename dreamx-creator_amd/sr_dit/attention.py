@@ -225,12 +225,15 @@ def _truncate_kv_cache(full_k, full_v, kv_len, L, f_kv):
 
 def _blockgrid_hip_attend(spec, q_i, full_k, full_v, *, anchor_k=None,
                           anchor_v=None, anchor_align="frame",
-                          anchor_window_scope="window"):
+                          anchor_window_scope="window", ring=None, sample=0):
     """Fused execution of one sample's windows -> ``[f_cur*h*w, n, d]``.
 
     Guards follow attention.py:842-863 and raise instead of degrading:
     not a GPU tensor, a head dim other than 64 or 128, autograd, a global
-    anchor scope, an unsupported dtype.
+    anchor scope, an unsupported dtype.  With ``ring`` (a ``KVRing`` whose
+    current region already holds the chunk) ``full_k``/``full_v`` are unused:
+    the anchor is written into the ring's prefix and the kernel reads the
+    cache in place.
     """
     f_cur, h, w = spec.f_cur, spec.h, spec.w
     n, d = q_i.shape[1], q_i.shape[2]
@@ -255,6 +258,14 @@ def _blockgrid_hip_attend(spec, q_i, full_k, full_v, *, anchor_k=None,
     anchor_mode = (None if not anchor_given
                    else ("frame" if anchor_align == "frame" else "chunk"))
     plan = _bgh.cached_plan(spec, anchor_mode=anchor_mode)
+    if ring is not None:
+        if anchor_given:
+            ring.write_anchor(sample, anchor_k, anchor_v)
+        out_i = q_i.new_empty(f_cur * h * w, n, d)
+        return _run_blockgrid_hip(
+            q_i.contiguous(), ring.k[sample], ring.v[sample], out_i, plan=plan, f_cur=f_cur,
+            h=h, w=w, n=n, d=d, anchor_mode=anchor_mode, ring=ring.kernel_ring(),
+            hr_base=ring.A)
     if anchor_given:
         k_ext = torch.cat([anchor_k, full_k], dim=0)
         v_ext = torch.cat([anchor_v, full_v], dim=0)
@@ -264,6 +275,25 @@ def _blockgrid_hip_attend(spec, q_i, full_k, full_v, *, anchor_k=None,
     return _run_blockgrid_hip(
         q_i.contiguous(), k_ext.contiguous(), v_ext.contiguous(), out_i,
         plan=plan, f_cur=f_cur, h=h, w=w, n=n, d=d, anchor_mode=anchor_mode)
+
+
+def _check_ring(ring, gs, b, n, d, pre_cache_k, pre_cache_v, kv_len):
+    """Argument checks of the in-place cache path (raise, never degrade)."""
+    if pre_cache_k is not None or pre_cache_v is not None:
+        raise ValueError("mask_free_window_attention: pass either kv_ring or "
+                         "pre_cache_k/pre_cache_v, not both.")
+    if kv_len is not None and int(kv_len) != ring.R:
+        raise ValueError(f"mask_free_window_attention: kv_len={kv_len} but the ring keeps "
+                         f"{ring.R} frames.")
+    if ring.batch != b or ring.n_heads != n or ring.head_dim != d:
+        raise ValueError("mask_free_window_attention: kv_ring shape does not match q.")
+    if any(list(g) != list(gs[0]) for g in gs):
+        raise ValueError("mask_free_window_attention: a kv_ring advances all samples "
+                         "together; grid_sizes must be equal.")
+    f_cur, h, w = (int(x) for x in gs[0])
+    if h * w != ring.L or f_cur > ring.F:
+        raise ValueError(f"mask_free_window_attention: grid {(f_cur, h, w)} does not fit the "
+                         f"ring ({ring.F} frames of {ring.L} tokens).")
 
 
 def mask_free_window_attention(
@@ -286,6 +316,8 @@ def mask_free_window_attention(
     block_radius_hw=(2, 2),
     block_radius_t=None,
     sym_radius_t=None,
+    kv_ring=None,
+    kv_commit=False,
 ):
     """Mask-free block-grid window self-attention with an optional KV cache.
 
@@ -298,6 +330,16 @@ def mask_free_window_attention(
 
     ``sym_radius_t`` (not in the reference): select the symmetric temporal
     rule, query frame ``t`` seeing frames ``[t - r, t + r]``.
+
+    ``kv_ring`` (not in the reference): a ``sr_dit.kv_ring.KVRing`` holding
+    the streaming cache in place of ``pre_cache_k``/``pre_cache_v``.  The
+    chunk's K/V go into the ring's current region (no copy when ``k``/``v``
+    already are those views), the attention reads the cache where it lies,
+    and with ``kv_commit`` the chunk is appended to the cache afterwards,
+    keeping the last ``kv_ring.R`` frames (the reference's cat + tail slice,
+    attention.py:1506-1510, :964-974).  The second and third return values
+    are then the ring itself.  A ring counts as a cache for the streaming
+    rule even while it is empty, as an empty cache tensor does.
     """
     b, s_cur, n, d = q.shape
     impl = str(attn_impl)
@@ -309,20 +351,27 @@ def mask_free_window_attention(
     outs, new_ck, new_cv = [], [], []
     anchor_hw_arg = None if anchor_hw is None else (int(anchor_hw[0]), int(anchor_hw[1]))
     gs = grid_sizes.tolist() if torch.is_tensor(grid_sizes) else [list(g) for g in grid_sizes]
+    if kv_ring is not None:
+        _check_ring(kv_ring, gs, b, n, d, pre_cache_k, pre_cache_v, kv_len)
     for i in range(b):
         f_cur, h, w = (int(x) for x in gs[i])
         if f_cur * h * w != s_cur:
             raise ValueError(f"grid {(f_cur, h, w)} inconsistent with s_cur={s_cur}")
         q_i, k_i, v_i = q[i], k[i], v[i]
-        if pre_cache_k is not None and pre_cache_v is not None:
-            full_k = torch.cat([pre_cache_k[i], k_i], dim=0)
-            full_v = torch.cat([pre_cache_v[i], v_i], dim=0)
+        if kv_ring is not None:
+            kv_ring.write_current(i, k_i, v_i)
+            full_k = full_v = None
+            f_kv = kv_ring.cached + f_cur
         else:
-            full_k, full_v = k_i, v_i
-        s_kv = full_k.shape[0]
-        f_kv = s_kv // (h * w)
-        if f_kv * h * w != s_kv:
-            raise ValueError("KV cache is not aligned to whole frames")
+            if pre_cache_k is not None and pre_cache_v is not None:
+                full_k = torch.cat([pre_cache_k[i], k_i], dim=0)
+                full_v = torch.cat([pre_cache_v[i], v_i], dim=0)
+            else:
+                full_k, full_v = k_i, v_i
+            s_kv = full_k.shape[0]
+            f_kv = s_kv // (h * w)
+            if f_kv * h * w != s_kv:
+                raise ValueError("KV cache is not aligned to whole frames")
 
         anchor_given = (anchor_k is not None) or (anchor_v is not None)
         use_anchor = anchor_given
@@ -360,7 +409,8 @@ def mask_free_window_attention(
         bt = int(block_t if block_t is not None else causal_chunk_frames)
         if bt <= 0:
             raise ValueError(f"block_t must be positive, got {bt}.")
-        is_streaming = (pre_cache_k is not None or pre_cache_v is not None or anchor_given)
+        is_streaming = (pre_cache_k is not None or pre_cache_v is not None or anchor_given
+                        or kv_ring is not None)
         hist = None if block_radius_t is None else (2 * int(block_radius_t) + 1) * bt
         if sym_radius_t is None:
             if hist is None:
@@ -389,12 +439,19 @@ def mask_free_window_attention(
             spec, q_i, full_k, full_v,
             anchor_k=(anchor_k[i] if use_anchor else None),
             anchor_v=(anchor_v[i] if use_anchor else None),
-            anchor_align=anchor_align, anchor_window_scope=anchor_window_scope)
+            anchor_align=anchor_align, anchor_window_scope=anchor_window_scope,
+            ring=kv_ring, sample=i)
         outs.append(out_i)
-        ck_i, cv_i = _truncate_kv_cache(full_k, full_v, kv_len, h * w, f_kv)
-        new_ck.append(ck_i)
-        new_cv.append(cv_i)
+        if kv_ring is None:
+            ck_i, cv_i = _truncate_kv_cache(full_k, full_v, kv_len, h * w, f_kv)
+            new_ck.append(ck_i)
+            new_cv.append(cv_i)
 
+    if kv_ring is not None:
+        if kv_commit:
+            kv_ring.commit(int(gs[0][0]))
+        out = outs[0].unsqueeze(0) if b == 1 else torch.stack(outs, 0)
+        return out, kv_ring, kv_ring
     if b == 1:
         return outs[0].unsqueeze(0), new_ck[0].unsqueeze(0), new_cv[0].unsqueeze(0)
     return torch.stack(outs, 0), torch.stack(new_ck, 0), torch.stack(new_cv, 0)

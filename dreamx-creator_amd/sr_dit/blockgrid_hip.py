@@ -240,7 +240,7 @@ def _device_tables(plan, device):
 
 
 def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
-                      anchor_mode=None, kernel="auto"):
+                      anchor_mode=None, kernel="auto", ring=None, hr_base=None):
     """Launch the fused window kernel for one sample; writes ``out`` and returns it.
 
     ``q``/``out``: ``[f_cur*h*w, n, d]``.  ``k_ext``/``v_ext``: the extended KV,
@@ -254,6 +254,14 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     members per workgroup sharing their K/V fetches) and everything else on
     the single-window kernel; ``"grouped"`` / ``"single"`` force one (a forced
     grouped launch of an anchored plan raises).
+
+    ``ring`` = ``(ring_frames, ring_cached, head)``: the HR KV after the anchor
+    prefix is an in-place cache (``sr_dit.kv_ring.KVRing``): ``ring_frames``
+    slots of ``h*w`` tokens, cached logical frame ``f`` in slot
+    ``(head[0] + f) % ring_frames``, then the current chunk's frames.  ``head``
+    is a device int32 tensor read by the kernel at launch.  ``hr_base``
+    overrides the plan's first HR token (a ring keeps its anchor prefix at a
+    fixed size whether or not a call uses it).
     """
     for name, t in (("q", q), ("k_ext", k_ext), ("v_ext", v_ext), ("out", out)):
         if not t.is_cuda:
@@ -269,7 +277,10 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     if k_ext.shape != v_ext.shape:
         raise ValueError("run_blockgrid_hip: k_ext and v_ext shapes differ.")
     params, order = _device_tables(plan, q.device)
-    hr_base = plan.get("hr_base", f_cur * h * w if anchor_mode is not None else 0)
+    if hr_base is None:
+        hr_base = plan.get("hr_base", f_cur * h * w if anchor_mode is not None else 0)
+    elif anchor_mode is not None and hr_base < plan.get("hr_base", 0):
+        raise ValueError("run_blockgrid_hip: hr_base leaves no room for the anchor prefix.")
     mode = 1 if anchor_mode == "frame" else 0
     if (plan["p_stride"] == P_FRAME) != (mode == 1):
         raise ValueError("run_blockgrid_hip: plan layout does not match anchor_mode.")
@@ -292,11 +303,11 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
         _lib.window_attn_grouped_fwd(
             q, k_ext, v_ext, out, params, groups, n_w=plan["n_w"], n_groups=groups.shape[0],
             hr_base=hr_base, H=h, W=w, n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0],
-            scale=d ** -0.5)
+            scale=d ** -0.5, ring=ring)
         return out
     _lib.window_attn_fwd(
         q, k_ext, v_ext, out, params, order,
         n_w=plan["n_w"], m_tiles=kernel_m_tiles(plan), p_stride=plan["p_stride"],
         hr_base=hr_base, H=h, W=w, n_heads=n, head_dim=d,
-        kv_tokens=k_ext.shape[0], scale=d ** -0.5, mode=mode)
+        kv_tokens=k_ext.shape[0], scale=d ** -0.5, mode=mode, ring=ring)
     return out
