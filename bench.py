@@ -44,6 +44,8 @@ def parse():
                     help="skip the SR-DiT refiner step (30 blocks, hipGraph) measurement")
     ap.add_argument("--no-prod", action="store_true",
                     help="skip the shipped-geometry (4x4 blocks, radius 3) window timings")
+    ap.add_argument("--no-stream", action="store_true",
+                    help="skip the streaming SR loop (chunks over the ring KV cache) measurement")
     ap.add_argument("--step-iters", type=int, default=5,
                     help="timed graph replays of the refiner step")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
@@ -139,20 +141,28 @@ def cpu_baseline(config, budget_s):
                        f"{med * 1e3:.1f} ms; os.cpu_count()={os.cpu_count()}; {cpu_model}")}
 
 
-def refiner_step(steps, warmup, layers=30):
+def build_model(layers=30):
+    """The 5B refiner (random weights, fp8 per-tensor Linears) and its build time."""
+    import torch
+    from sr_dit import model as mdl
+
+    t0 = time.perf_counter()
+    model = mdl.build_refiner(mdl.SRDiTConfig(num_layers=layers), device=torch.device("cuda:0"),
+                              scaling="tensor", seed=0)
+    return model, time.perf_counter() - t0
+
+
+def refiner_step(model, build_s, steps, warmup):
     """One SR-DiT 5B refiner step at 2K: 30 blocks + head on 21,600 tokens with 512
     context tokens, fp8 per-tensor linears, window self-attention as in c3, dense
     cross-attention, captured once in a HIP graph and replayed."""
     import torch
-    from sr_dit import model as mdl
     from sr_dit import workloads as wl
     from sr_dit.fp8_linear import Fp8Linear
 
     dev = torch.device("cuda:0")
-    cfg = mdl.SRDiTConfig(num_layers=layers)
-    t0 = time.perf_counter()
-    model = mdl.build_refiner(cfg, device=dev, scaling="tensor", seed=0)
-    build_s = time.perf_counter() - t0
+    cfg = model.cfg
+    layers = cfg.num_layers
     f, h, w = 6, 45, 80
     s_tok = f * h * w
     geom = model.geometry(f, h, w, cfg.text_len, dev)
@@ -203,6 +213,54 @@ def refiner_step(steps, warmup, layers=30):
             "gemm_tflop": round(gemm / 1e12, 2), "tflops": round(total / (ms * 1e-3) / 1e12, 1),
             "build_s": round(build_s, 1),
             "data": "synthetic: N(0,0.02) weights, N(0,1) activations and context"}
+
+
+def stream_chunks(model, chunks=6, timed=2):
+    """The streaming SR loop at the shipped settings: 45x80-token frames (90x160
+    latent), 3-frame chunks, a 9-frame KV cache per layer kept in place (ring),
+    4x4-block radius-3 windows, the warped 4-step schedule plus the refresh pass
+    per chunk (5 forwards of the 30-layer model), every forward a HIP graph
+    replay.  The first chunks fill the cache (one graph per cache length); the
+    last ``timed`` chunks run at the full 12-frame KV and are timed."""
+    import torch
+    from sr_dit.stream import StreamingRefiner
+
+    dev = torch.device("cuda:0")
+    cfg = model.cfg
+    h, w, chunk = 45, 80, 3
+    g = torch.Generator("cpu").manual_seed(0)
+    noise = torch.randn(cfg.in_dim, chunk * chunks, 2 * h, 2 * w, generator=g).to(dev)
+    ctx = torch.randn(cfg.text_len, cfg.text_dim, generator=g).to(torch.bfloat16).to(dev)
+    t0 = time.perf_counter()
+    r = StreamingRefiner(model, h, w, ctx, chunk=chunk, kv_len=9, device=dev)
+    per_chunk = []
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    for c in range(chunks):
+        e0.record()
+        r.refine_chunk(noise[:, c * chunk:(c + 1) * chunk], c * chunk)
+        e1.record()
+        torch.cuda.synchronize()
+        per_chunk.append(e0.elapsed_time(e1))
+    wall = time.perf_counter() - t0
+    steady = per_chunk[-timed:]
+    ms = sum(steady) / len(steady)
+    # one eager forward at the full cache for comparison
+    r.use_graph = False
+    e0.record()
+    r.forward(noise[:, :chunk], r.steps[0], chunks * chunk)
+    e1.record()
+    torch.cuda.synchronize()
+    eager_fwd = e0.elapsed_time(e1)
+    return {"workload": "streaming SR loop, 5B refiner (30 layers), 3 x 45x80-token chunk vs "
+                        "9 cached frames (ring), 4x4 blocks radius 3, 4 denoising steps + "
+                        "KV refresh per chunk, 512 context tokens",
+            "ms_per_chunk": round(ms, 2), "ms_per_forward": round(ms / (len(r.steps) + 1), 2),
+            "eager_ms_per_forward": round(eager_fwd, 2), "forwards_per_chunk": len(r.steps) + 1,
+            "steps": [round(t, 2) for t in r.steps], "kv_frames": 9 + chunk,
+            "chunk_ms_all": [round(x, 1) for x in per_chunk], "hip_graphs": len(r._graphs),
+            "wall_s": round(wall, 1),
+            "data": "synthetic: N(0,0.02) weights, N(0,1) noise latents and context"}
 
 
 def production_window(steps, warmup=3):
@@ -336,8 +394,13 @@ def main():
     }
     if not args.no_prod:
         result["production_window"] = production_window(20)
-    if not args.no_step:
-        result["refiner_step"] = refiner_step(args.step_iters, 1)
+    if not (args.no_step and args.no_stream):
+        model, build_s = build_model()
+        if not args.no_step:
+            result["refiner_step"] = refiner_step(model, build_s, args.step_iters, 1)
+        if not args.no_stream:
+            result["stream"] = stream_chunks(model)
+        del model
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     print(json.dumps(result), flush=True)

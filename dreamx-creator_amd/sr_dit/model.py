@@ -241,10 +241,19 @@ class Block(nn.Module):
                 self.ffn[0], self.ffn[2])
         return all(isinstance(m, Fp8Linear) and m.scaling == "tensor" for m in lins)
 
-    def forward(self, x, e, context, geom):
-        """x [s, dim] (bf16), e [1, 6, dim] (fp32), context [lc, dim] -> [s, dim]."""
+    def forward(self, x, e, context, geom, ring=None, cross_kv=None):
+        """x [s, dim] (bf16), e [1, 6, dim] (fp32), context [lc, dim] -> [s, dim].
+
+        ``ring``: this layer's streaming KV cache (``KVRing``, fused path only);
+        ``cross_kv``: this layer's text K/V, computed once per video
+        (``SRDiT.cross_cache``) as WanT2VCrossAttention.init_cache
+        (models.py:1035-1040) keeps them.
+        """
         if FUSED and x.dtype == torch.bfloat16 and self.fusable():
-            return self.forward_fused(x, e, context, geom)
+            return self.forward_fused(x, e, context, geom, ring=ring, cross_kv=cross_kv)
+        if ring is not None or cross_kv is not None:
+            raise ValueError("Block: the streaming cache and the cached text K/V need the fused "
+                             "forward (bf16 activations, per-tensor Fp8Linear).")
         dt = x.dtype
         ep = (self.modulation.float() + e).chunk(6, dim=1)
         ep = [t.reshape(1, -1) for t in ep]
@@ -257,7 +266,7 @@ class Block(nn.Module):
         return (x.float() + y.float() * ep[5]).to(dt)
 
 
-    def forward_fused(self, x, e, context, geom):
+    def forward_fused(self, x, e, context, geom, ring=None, cross_kv=None):
         """The same block with the elementwise chains fused into single-pass kernels.
 
         LayerNorm + modulation (+ the amax of its output), RMSNorm + RoPE and
@@ -268,6 +277,10 @@ class Block(nn.Module):
         output; one call then applies the GELU in place (once per element),
         reduces the amax and writes the e4m3 codes the second GEMM reads.  The arithmetic at each point is the reference's
         (models.py:1304-1351); only reduction orders differ.
+
+        With a ``ring`` the RMSNorm + RoPE kernel writes K, and the V GEMM
+        writes V, straight into the ring's current-chunk region, and the window
+        kernel reads the cached frames in place (no concatenation).
         """
         sa, ca = self.self_attn, self.cross_attn
         cfg = sa.cfg
@@ -289,14 +302,30 @@ class Block(nn.Module):
         attn_in = torch.empty(s, dim, dtype=bf, device=dev)
         _lib.ln_modulate(x, None, None, mod[1], mod[0], self.norm1.eps, attn_in, a0)
         xq, xs = quant_from(attn_in, a0)
-        q_lin, k_lin, v = sa.q.gemm(xq, xs), sa.k.gemm(xq, xs), sa.v.gemm(xq, xs)
+        q_lin, k_lin = sa.q.gemm(xq, xs), sa.k.gemm(xq, xs)
+        if ring is None:
+            v = sa.v.gemm(xq, xs)
+            k = torch.empty(s, dim, dtype=bf, device=dev)
+        else:
+            v = sa.v.gemm(xq, xs, out=ring.current_v(0, f).view(s, dim))
+            k = ring.current_k(0, f).view(s, dim)
         q = torch.empty(s, dim, dtype=bf, device=dev)
-        k = torch.empty(s, dim, dtype=bf, device=dev)
         _lib.rmsnorm_rope(q_lin, sa.norm_q.weight, sa.norm_q.eps, geom["rope_cs"], d, q)
         _lib.rmsnorm_rope(k_lin, sa.norm_k.weight, sa.norm_k.eps, geom["rope_cs"], d, k)
         att_out = torch.empty(s, n, d, dtype=bf, device=dev)
-        bgh.run_blockgrid_hip(q.view(s, n, d), k.view(s, n, d), v.view(s, n, d), att_out,
-                              plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d)
+        if ring is None:
+            bgh.run_blockgrid_hip(q.view(s, n, d), k.view(s, n, d), v.view(s, n, d), att_out,
+                                  plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d)
+        elif geom.get("ring_cat"):
+            # the reference's concatenation of the cache with the chunk (tests only)
+            lk, lv = ring.logical(0)
+            bgh.run_blockgrid_hip(q.view(s, n, d), torch.cat([lk, k.view(s, n, d)]),
+                                  torch.cat([lv, v.view(s, n, d)]), att_out, plan=geom["plan"],
+                                  f_cur=f, h=h, w=w, n=n, d=d)
+        else:
+            bgh.run_blockgrid_hip(q.view(s, n, d), ring.k[0], ring.v[0], att_out,
+                                  plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d,
+                                  ring=ring.kernel_ring(), hr_base=ring.A)
         y = sa.o(att_out.view(s, dim))
         x1 = torch.empty_like(x)
         _lib.residual_gate(x, y, mod[2], x1)
@@ -308,10 +337,7 @@ class Block(nn.Module):
         cq = torch.empty(s, dim, dtype=bf, device=dev)
         _lib.rmsnorm_rope(ca.q.gemm(xq, xs), ca.norm_q.weight, ca.norm_q.eps, None, d, cq)
         lc = context.shape[0]
-        cxq, cxs = quantize_tensor(context, geom["amax_ctx"])
-        ck = torch.empty(lc, dim, dtype=bf, device=dev)
-        _lib.rmsnorm_rope(ca.k.gemm(cxq, cxs), ca.norm_k.weight, ca.norm_k.eps, None, d, ck)
-        cv = ca.v.gemm(cxq, cxs)
+        ck, cv = self.cross_kv(context, geom) if cross_kv is None else cross_kv
         c_out = torch.empty(s, n, d, dtype=bf, device=dev)
         geom["cross"].run(cq.view(s, n, d), ck.view(lc, n, d), cv.view(lc, n, d), c_out)
         co = ca.o(c_out.view(s, dim))
@@ -330,6 +356,16 @@ class Block(nn.Module):
         x3 = torch.empty_like(x)
         _lib.residual_gate(x2, y2, mod[5], x3)
         return x3
+
+    def cross_kv(self, context, geom):
+        """The cross-attention's text K (RMSNorm'd) and V, [lc, dim] bf16 each."""
+        ca = self.cross_attn
+        lc, dim = context.shape
+        cxq, cxs = quantize_tensor(context, geom["amax_ctx"])
+        ck = torch.empty(lc, dim, dtype=torch.bfloat16, device=context.device)
+        _lib.rmsnorm_rope(ca.k.gemm(cxq, cxs), ca.norm_k.weight, ca.norm_k.eps, None,
+                          ca.cfg.head_dim, ck)
+        return ck, ca.v.gemm(cxq, cxs)
 
 
 #: Use the fused block forward when a block's Linears are all per-tensor Fp8Linear.
@@ -383,6 +419,25 @@ class SRDiT(nn.Module):
                                   bh=cfg.block_hw[0], bw=cfg.block_hw[1],
                                   rh=cfg.block_radius_hw[0], rw=cfg.block_radius_hw[1],
                                   sym_rt=cfg.sym_radius_t)
+        return self._geometry(spec, lc, device, t_offset)
+
+    def stream_geometry(self, f, h, w, lc, device, *, cached, chunk=3, t_offset=0,
+                        block_hw=(4, 4), block_radius_hw=(3, 3)):
+        """Geometry of one streaming chunk: ``f`` query frames against ``cached``
+        cached frames plus themselves, under the reference's streaming rule with
+        ``block_t = chunk`` and ``rt = f_kv // chunk - 1`` (attention.py:1575-1604
+        as models.py:651-676 calls it; the shipped window is 4x4 blocks, radius 3,
+        sr_dit_5b.yaml:45-55)."""
+        f_kv = int(cached) + f
+        spec = att._BlockGridSpec(f_cur=f, f_kv=f_kv, h=h, w=w, block_t=chunk,
+                                  bh=block_hw[0], bw=block_hw[1],
+                                  rh=block_radius_hw[0], rw=block_radius_hw[1],
+                                  rt=max(f_kv // chunk - 1, 0), streaming=True)
+        return self._geometry(spec, lc, device, t_offset)
+
+    def _geometry(self, spec, lc, device, t_offset):
+        cfg = self.cfg
+        f, h, w = spec.f_cur, spec.h, spec.w
         rope = rope_table(cfg, f, h, w, t_offset, device)
         return {"grid": (f, h, w), "plan": bgh.cached_plan(spec),
                 "cross": CrossAttentionPlan(f * h * w, lc),
@@ -396,32 +451,64 @@ class SRDiT(nn.Module):
 
     # -- forward pieces -----------------------------------------------------
     def time_embed(self, t):
-        """t [1] -> (e [1, dim], e0 [1, 6, dim]), fp32 (models.py:1845-1849)."""
-        e = self.time_embedding(sinusoidal_embedding_1d(self.cfg.freq_dim, t).float())
-        e0 = self.time_projection(e).unflatten(1, (6, self.cfg.dim))
+        """t [1] -> (e [1, dim], e0 [1, 6, dim]), fp32 whatever the weights' dtype, as
+        the reference's fp32 autocast region computes them (models.py:1845-1849)."""
+        def lin(m, x):
+            return F.linear(x, m.weight.float(), None if m.bias is None else m.bias.float())
+
+        te, tp = self.time_embedding, self.time_projection
+        e = lin(te[2], F.silu(lin(te[0], sinusoidal_embedding_1d(self.cfg.freq_dim, t).float())))
+        e0 = lin(tp[1], F.silu(e)).unflatten(1, (6, self.cfg.dim))
         return e, e0
 
-    def blocks_forward(self, x, e0, context, geom):
-        """The 30-block stack: x [s, dim] bf16 -> [s, dim]."""
-        for blk in self.blocks:
-            x = blk(x, e0, context, geom)
+    def blocks_forward(self, x, e0, context, geom, rings=None, cross=None):
+        """The 30-block stack: x [s, dim] bf16 -> [s, dim].  ``rings``/``cross``:
+        per-layer streaming KV caches and cached text K/V (or None)."""
+        for i, blk in enumerate(self.blocks):
+            x = blk(x, e0, context, geom, ring=None if rings is None else rings[i],
+                    cross_kv=None if cross is None else cross[i])
         return x
 
-    def forward(self, latent, t, context_raw, geom):
-        """latent [in_dim, f, 2h, 2w] -> [out_dim, f, 2h, 2w] (one sample)."""
+    def embed_patches(self, latent):
+        """The patch-embedding Conv3d (models.py:1551-1552; kernel = stride = patch)
+        as the GEMM it is: latent [C, F, ph*h, pw*w] -> tokens [F*h*w, dim] in
+        (frame, row, column) order, and the token grid.  A plain GEMM also
+        captures in a HIP graph."""
+        pt, ph, pw = self.cfg.patch_size
+        wgt = self.patch_embedding.weight
+        c, fr, hh, ww = latent.shape
+        f, h, w = fr // pt, hh // ph, ww // pw
+        patches = (latent.to(wgt.dtype).view(c, f, pt, h, ph, w, pw)
+                   .permute(1, 3, 5, 0, 2, 4, 6).reshape(f * h * w, c * pt * ph * pw))
+        x = F.linear(patches, wgt.reshape(wgt.shape[0], -1), self.patch_embedding.bias)
+        return x.contiguous(), (f, h, w)
+
+    def embed_text(self, context_raw):
+        """Text embedding of the padded context (models.py:1860-1866): [lc, dim]."""
         cfg = self.cfg
         dt = self.patch_embedding.weight.dtype
-        x = self.patch_embedding(latent.unsqueeze(0).to(dt))
-        f, h, w = x.shape[2:]
-        x = x.flatten(2).transpose(1, 2)[0].contiguous()
         ctx = context_raw
         if ctx.shape[0] < cfg.text_len:
             ctx = torch.cat([ctx, ctx.new_zeros(cfg.text_len - ctx.shape[0], ctx.shape[1])])
-        ctx = self.text_embedding(ctx.to(dt))
+        return self.text_embedding(ctx.to(dt))
+
+    def cross_cache(self, ctx, geom):
+        """Every layer's cross-attention K/V of the embedded context, computed once
+        and reused by every step (WanT2VCrossAttention.init_cache, models.py:1035-1040)."""
+        return [blk.cross_kv(ctx, geom) for blk in self.blocks]
+
+    def forward_embedded(self, latent, e, e0, ctx, geom, rings=None, cross=None):
+        """Patch embedding, blocks and head for an embedded context and timestep:
+        latent [in_dim, f, 2h, 2w] -> [out_dim, f, 2h, 2w] fp32."""
+        cfg = self.cfg
+        x, (f, h, w) = self.embed_patches(latent)
+        x = self.blocks_forward(x, e0, ctx, geom, rings=rings, cross=cross)
+        return unpatchify(self.head(x, e), (f, h, w), cfg.patch_size, cfg.out_dim)
+
+    def forward(self, latent, t, context_raw, geom):
+        """latent [in_dim, f, 2h, 2w] -> [out_dim, f, 2h, 2w] (one sample)."""
         e, e0 = self.time_embed(t)
-        x = self.blocks_forward(x, e0, ctx, geom)
-        y = self.head(x, e)
-        return unpatchify(y, (f, h, w), cfg.patch_size, cfg.out_dim)
+        return self.forward_embedded(latent, e, e0, self.embed_text(context_raw), geom)
 
 
 def unpatchify(x, grid, patch_size, c):
