@@ -23,13 +23,12 @@
 // accumulator holds out^T: each lane owns one output row and runs of four
 // consecutive columns, stored as 8-byte bf16 quads.
 #include "common.h"
+#include "fp8_common.h"
 
 namespace srdit {
 namespace {
 
-constexpr float kFp8Max = 448.f;
-constexpr float kInvFp8Max = 1.0f / 448.0f;   // fl32(1/448), folded at compile time
-constexpr float kScaleFloor = 1e-12f;
+using namespace q8;
 
 // ---------------------------------------------------------------- quantisers
 
@@ -78,27 +77,6 @@ __device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
   return v;
 }
 
-// scale = max(amax * fl32(1/448), 1e-12); a NaN amax stays NaN as torch's clamp_min keeps it.
-__device__ __forceinline__ float scale_from_amax_bits(uint32_t bits) {
-  const float s = __uint_as_float(bits) * kInvFp8Max;
-  return s < kScaleFloor ? kScaleFloor : s;
-}
-
-__device__ __forceinline__ float clamp_fp8(float q) {
-  return q > kFp8Max ? kFp8Max : (q < -kFp8Max ? -kFp8Max : q);
-}
-
-// Eight values -> eight e4m3 bytes (round to nearest even).
-__device__ __forceinline__ uint2 to_e4m3x8(const float f[8], float s) {
-  float q[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = clamp_fp8(f[i] / s);
-  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
-  lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
-  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
-  hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
-  return make_uint2((uint32_t)lo, (uint32_t)hi);
-}
 
 // One wavefront per row, four rows per workgroup.  The second pass re-reads
 // the row, which is still in the L1/L2 after the first.
