@@ -197,6 +197,21 @@ __device__ __forceinline__ LaneOff<D> make_lane_offsets(int wave) {
 //   token = base + (t0 + j/sp)*frame_len + (r0 + (j%sp)/cols)*Wg + c0 + (j%sp)%cols
 // The HR cuboid, the anchor prefix of the plain kernel and an anchor segment of
 // the frame kernel are all this formula with their own grid.
+// Max |value| of the output, as fp32 bits (non-negative floats order like their
+// bits; a NaN sorts above infinity, so it wins as in torch's amax): the
+// wavefront's maximum goes to *amax with one atomicMax from lane 0.
+template <typename H2>
+__device__ __forceinline__ uint32_t abs_bits2(H2 v) {
+  const f32x2_t f = __builtin_convertvector(v, f32x2_t);
+  return max(__float_as_uint(f[0]) & 0x7fffffffu, __float_as_uint(f[1]) & 0x7fffffffu);
+}
+
+__device__ __forceinline__ void wave_amax_out(uint32_t* amax, uint32_t m) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), o)));
+  if ((threadIdx.x & 63) == 0) atomicMax(amax, m);
+}
+
 // Frame layout of a streaming KV cache kept in place: R ring slots holding the
 // nc cached frames (oldest first, cached frame f in slot (head + f) mod R),
 // followed by the current chunk's frames (logical frame nc + i at R + i).

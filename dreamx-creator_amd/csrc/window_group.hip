@@ -44,6 +44,7 @@ struct GroupArgs {
   float scale_log2;  // softmax scale * log2(e)
   int ring_R, ring_nc;       // in-place KV cache layout (ring_R == 0: plain)
   const int32_t* ring_head;  // device int32: ring slot of the oldest cached frame
+  uint32_t* amax_out;        // max |O| bits, or null
 };
 
 constexpr int GKN = 32;  // keys per block
@@ -494,22 +495,33 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   // O = acc / l ; lane (c, hf) writes dims dt*32 + 8*g4 + 4*hf + [0, 4) of its query
   const float lt = half_sum(lrun);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  if (!qvalid) return;
-  T* op = reinterpret_cast<T*>(a.o) + head * D + qflat * tok;
+  uint32_t am = 0;
+  if (qvalid) {
+    T* op = reinterpret_cast<T*>(a.o) + head * D + qflat * tok;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const f32x2_t lo2 = {oacc[dt][g4 * 4 + 0] * inv, oacc[dt][g4 * 4 + 1] * inv};
-      const f32x2_t hi2 = {oacc[dt][g4 * 4 + 2] * inv, oacc[dt][g4 * 4 + 3] * inv};
-      const i32x2_t w = {__builtin_bit_cast(int, __builtin_convertvector(lo2, typename E::h2)),
-                         __builtin_bit_cast(int, __builtin_convertvector(hi2, typename E::h2))};
-      *reinterpret_cast<i32x2_t*>(op + dt * 32 + g4 * 8 + hf * 4) = w;
-    }
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const f32x2_t lo2 = {oacc[dt][g4 * 4 + 0] * inv, oacc[dt][g4 * 4 + 1] * inv};
+        const f32x2_t hi2 = {oacc[dt][g4 * 4 + 2] * inv, oacc[dt][g4 * 4 + 3] * inv};
+        const auto l = __builtin_convertvector(lo2, typename E::h2);
+        const auto u = __builtin_convertvector(hi2, typename E::h2);
+        const i32x2_t w = {__builtin_bit_cast(int, l), __builtin_bit_cast(int, u)};
+        *reinterpret_cast<i32x2_t*>(op + dt * 32 + g4 * 8 + hf * 4) = w;
+        if (a.amax_out) am = max(am, max(abs_bits2(l), abs_bits2(u)));
+      }
+  }
+  if (a.amax_out) wave_amax_out(a.amax_out, am);
 }
+
+__global__ void clear_amax_kernel(uint32_t* p) { *p = 0u; }
 
 template <typename T, int D>
 int launch_group(const GroupArgs& a, uint32_t grid, hipStream_t stream) {
+  if (a.amax_out) {
+    hipLaunchKernelGGL(clear_amax_kernel, dim3(1), dim3(1), 0, stream, a.amax_out);
+    SRDIT_LAUNCH_CHECK("clear_amax_kernel");
+  }
   hipLaunchKernelGGL((window_group_kernel<T, D>), dim3(grid), dim3(256), 0, stream, a);
   SRDIT_LAUNCH_CHECK("window_group_kernel");
   return SRDIT_OK;
@@ -524,8 +536,8 @@ namespace {
 int group_entry(const char* fn, const void* q, const void* k, const void* v, void* o,
                 const int32_t* params, const int32_t* groups, int n_w, int n_groups, int hr_base,
                 int H, int W, int64_t q_tokens, int64_t kv_tokens, int n_heads, int head_dim,
-                float scale, int ring_R, int ring_nc, const int32_t* ring_head, int dtype,
-                void* stream) {
+                float scale, int ring_R, int ring_nc, const int32_t* ring_head,
+                uint32_t* amax_out, int dtype, void* stream) {
   SRDIT_REQUIRE(q && k && v && o && params && groups, "%s: null pointer", fn);
   SRDIT_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
                 "%s: q/k/v/o must be 16-byte aligned", fn);
@@ -557,7 +569,7 @@ int group_entry(const char* fn, const void* q, const void* k, const void* v, voi
   a.n_w = n_w; a.n_groups = n_groups; a.hr_base = hr_base; a.H = H; a.W = W;
   a.q_tokens = q_tokens; a.kv_tokens = kv_tokens; a.n_heads = n_heads;
   a.scale_log2 = scale * 1.4426950408889634f;
-  a.ring_R = ring_R; a.ring_nc = ring_nc; a.ring_head = ring_head;
+  a.ring_R = ring_R; a.ring_nc = ring_nc; a.ring_head = ring_head; a.amax_out = amax_out;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint32_t grid = static_cast<uint32_t>(grid64);
   if (dtype == SRDIT_DTYPE_BF16)
@@ -575,27 +587,30 @@ extern "C" int srdit_window_attn_grouped_fwd(const void* q, const void* k, const
                                              int head_dim, float scale, int dtype, void* stream) {
   return srdit::group_entry("srdit_window_attn_grouped_fwd", q, k, v, o, params, groups, n_w,
                             n_groups, hr_base, H, W, q_tokens, kv_tokens, n_heads, head_dim,
-                            scale, 0, 0, nullptr, dtype, stream);
+                            scale, 0, 0, nullptr, nullptr, dtype, stream);
 }
 
-extern "C" int srdit_window_attn_grouped_ring_fwd(const void* q, const void* k, const void* v,
-                                                  void* o, const int32_t* params,
-                                                  const int32_t* groups, int n_w, int n_groups,
-                                                  int hr_base, int H, int W, int64_t q_tokens,
-                                                  int64_t kv_tokens, int n_heads, int head_dim,
-                                                  float scale, int ring_frames, int ring_cached,
-                                                  const int32_t* ring_head, int dtype,
-                                                  void* stream) {
+extern "C" int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, const void* v,
+                                                void* o, const int32_t* params,
+                                                const int32_t* groups, int n_w, int n_groups,
+                                                int hr_base, int H, int W, int64_t q_tokens,
+                                                int64_t kv_tokens, int n_heads, int head_dim,
+                                                float scale, int ring_frames, int ring_cached,
+                                                const int32_t* ring_head, uint32_t* amax_out,
+                                                int dtype, void* stream) {
   using namespace srdit;
-  SRDIT_REQUIRE(ring_head != nullptr, "srdit_window_attn_grouped_ring_fwd: null ring_head");
-  SRDIT_REQUIRE(ring_frames >= 1 && ring_cached >= 0 && ring_cached <= ring_frames,
-                "srdit_window_attn_grouped_ring_fwd: need 1 <= ring_frames and 0 <= ring_cached "
-                "<= ring_frames (got %d, %d)", ring_frames, ring_cached);
-  SRDIT_REQUIRE(hr_base >= 0 && static_cast<int64_t>(hr_base) +
-                    static_cast<int64_t>(ring_frames) * H * W <= kv_tokens,
-                "srdit_window_attn_grouped_ring_fwd: kv_tokens %lld do not cover the anchor "
-                "prefix and %d ring frames", static_cast<long long>(kv_tokens), ring_frames);
-  return group_entry("srdit_window_attn_grouped_ring_fwd", q, k, v, o, params, groups, n_w,
-                     n_groups, hr_base, H, W, q_tokens, kv_tokens, n_heads, head_dim, scale,
-                     ring_frames, ring_cached, ring_head, dtype, stream);
+  const char* fn = "srdit_window_attn_grouped_fwd_ex";
+  if (ring_frames != 0) {
+    SRDIT_REQUIRE(ring_head != nullptr, "%s: null ring_head", fn);
+    SRDIT_REQUIRE(ring_frames >= 1 && ring_cached >= 0 && ring_cached <= ring_frames,
+                  "%s: need 0 <= ring_cached <= ring_frames (got %d, %d)", fn, ring_cached,
+                  ring_frames);
+    SRDIT_REQUIRE(hr_base >= 0 && static_cast<int64_t>(hr_base) +
+                      static_cast<int64_t>(ring_frames) * H * W <= kv_tokens,
+                  "%s: kv_tokens %lld do not cover the anchor prefix and %d ring frames", fn,
+                  static_cast<long long>(kv_tokens), ring_frames);
+  }
+  return group_entry(fn, q, k, v, o, params, groups, n_w, n_groups, hr_base, H, W, q_tokens,
+                     kv_tokens, n_heads, head_dim, scale, ring_frames, ring_cached, ring_head,
+                     amax_out, dtype, stream);
 }

@@ -28,14 +28,14 @@ SIGNATURES = {
     "srdit_window_attn_grouped_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_int,
                                                _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_int,
                                                _c_int, _c_f, _c_int, _c_p]),
-    "srdit_window_attn_ring_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
-                                            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                            _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_int,
-                                            _c_int, _c_int, _c_p, _c_int, _c_p]),
-    "srdit_window_attn_grouped_ring_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int,
-                                                    _c_int, _c_int, _c_int, _c_int, _c_i64,
-                                                    _c_i64, _c_int, _c_int, _c_f, _c_int, _c_int,
-                                                    _c_p, _c_int, _c_p]),
+    "srdit_window_attn_fwd_ex": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                          _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                          _c_i64, _c_i64, _c_int, _c_int, _c_f, _c_int,
+                                          _c_int, _c_int, _c_p, _c_p, _c_int, _c_p]),
+    "srdit_window_attn_grouped_fwd_ex": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int,
+                                                  _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64,
+                                                  _c_int, _c_int, _c_f, _c_int, _c_int, _c_p,
+                                                  _c_p, _c_int, _c_p]),
     "srdit_fp8_quant_rowwise": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p]),
     "srdit_fp8_quant_tensor": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
                                         _c_p]),
@@ -99,17 +99,24 @@ def _stream(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _ring_args(ring):
-    """``ring`` = (ring_frames, ring_cached, head) with ``head`` a device int32 tensor."""
-    R, nc, head = ring
-    if not (torch.is_tensor(head) and head.dtype == torch.int32 and head.is_cuda
-            and head.numel() >= 1):
-        raise ValueError("ring head must be a device int32 tensor")
-    return int(R), int(nc), head.data_ptr()
+def _ex_args(ring, amax_out):
+    """Trailing arguments of the _ex entry points: ``ring`` = (ring_frames,
+    ring_cached, head) with ``head`` a device int32 tensor, or None;
+    ``amax_out`` a device int32 [1] word, or None."""
+    if ring is None:
+        R, nc, head = 0, 0, None
+    else:
+        R, nc, head = ring
+        if not (torch.is_tensor(head) and head.dtype == torch.int32 and head.is_cuda
+                and head.numel() >= 1):
+            raise ValueError("ring head must be a device int32 tensor")
+    if amax_out is not None and not (amax_out.dtype == torch.int32 and amax_out.is_cuda):
+        raise ValueError("amax_out must be a device int32 word")
+    return int(R), int(nc), _ptr(head), _ptr(amax_out)
 
 
 def window_attn_fwd(q, k, v, o, params, order, *, n_w, m_tiles, p_stride, hr_base,
-                    H, W, n_heads, head_dim, kv_tokens, scale, mode, ring=None):
+                    H, W, n_heads, head_dim, kv_tokens, scale, mode, ring=None, amax_out=None):
     if q.dtype not in DTYPE_CODES:
         raise ValueError(f"window attention needs bf16 or fp16, got {q.dtype}")
     args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(params), _ptr(order),
@@ -117,27 +124,27 @@ def window_attn_fwd(q, k, v, o, params, order, *, n_w, m_tiles, p_stride, hr_bas
             int(q.shape[0]), int(kv_tokens), int(n_heads), int(head_dim), float(scale),
             int(mode))
     tail = (DTYPE_CODES[q.dtype], _stream(q.device))
-    if ring is None:
+    if ring is None and amax_out is None:
         _check(load().srdit_window_attn_fwd(*args, *tail), "srdit_window_attn_fwd")
     else:
-        _check(load().srdit_window_attn_ring_fwd(*args, *_ring_args(ring), *tail),
-               "srdit_window_attn_ring_fwd")
+        _check(load().srdit_window_attn_fwd_ex(*args, *_ex_args(ring, amax_out), *tail),
+               "srdit_window_attn_fwd_ex")
 
 
 def window_attn_grouped_fwd(q, k, v, o, params, groups, *, n_w, n_groups, hr_base, H, W,
-                            n_heads, head_dim, kv_tokens, scale, ring=None):
+                            n_heads, head_dim, kv_tokens, scale, ring=None, amax_out=None):
     if q.dtype not in DTYPE_CODES:
         raise ValueError(f"window attention needs bf16 or fp16, got {q.dtype}")
     args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(params), _ptr(groups),
             int(n_w), int(n_groups), int(hr_base), int(H), int(W), int(q.shape[0]),
             int(kv_tokens), int(n_heads), int(head_dim), float(scale))
     tail = (DTYPE_CODES[q.dtype], _stream(q.device))
-    if ring is None:
+    if ring is None and amax_out is None:
         _check(load().srdit_window_attn_grouped_fwd(*args, *tail),
                "srdit_window_attn_grouped_fwd")
     else:
-        _check(load().srdit_window_attn_grouped_ring_fwd(*args, *_ring_args(ring), *tail),
-               "srdit_window_attn_grouped_ring_fwd")
+        _check(load().srdit_window_attn_grouped_fwd_ex(*args, *_ex_args(ring, amax_out), *tail),
+               "srdit_window_attn_grouped_fwd_ex")
 
 
 QUANT_DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

@@ -240,7 +240,8 @@ def _device_tables(plan, device):
 
 
 def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
-                      anchor_mode=None, kernel="auto", ring=None, hr_base=None):
+                      anchor_mode=None, kernel="auto", ring=None, hr_base=None,
+                      amax_out=None):
     """Launch the fused window kernel for one sample; writes ``out`` and returns it.
 
     ``q``/``out``: ``[f_cur*h*w, n, d]``.  ``k_ext``/``v_ext``: the extended KV,
@@ -261,7 +262,8 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     ``(head[0] + f) % ring_frames``, then the current chunk's frames.  ``head``
     is a device int32 tensor read by the kernel at launch.  ``hr_base``
     overrides the plan's first HR token (a ring keeps its anchor prefix at a
-    fixed size whether or not a call uses it).
+    fixed size whether or not a call uses it).  ``amax_out`` (device int32
+    [1]): receives the bits of max |out| for a per-tensor quantiser of it.
     """
     for name, t in (("q", q), ("k_ext", k_ext), ("v_ext", v_ext), ("out", out)):
         if not t.is_cuda:
@@ -303,11 +305,11 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
         _lib.window_attn_grouped_fwd(
             q, k_ext, v_ext, out, params, groups, n_w=plan["n_w"], n_groups=groups.shape[0],
             hr_base=hr_base, H=h, W=w, n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0],
-            scale=d ** -0.5, ring=ring)
+            scale=d ** -0.5, ring=ring, amax_out=amax_out)
         return out
     _lib.window_attn_fwd(
         q, k_ext, v_ext, out, params, order,
         n_w=plan["n_w"], m_tiles=kernel_m_tiles(plan), p_stride=plan["p_stride"],
         hr_base=hr_base, H=h, W=w, n_heads=n, head_dim=d,
-        kv_tokens=k_ext.shape[0], scale=d ** -0.5, mode=mode, ring=ring)
+        kv_tokens=k_ext.shape[0], scale=d ** -0.5, mode=mode, ring=ring, amax_out=amax_out)
     return out

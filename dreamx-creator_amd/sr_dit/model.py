@@ -158,9 +158,9 @@ class CrossAttentionPlan:
                      "block_m": 64, "m_tiles": 1, "block_n": 64, "hr_base": 0,
                      "p_stride": bgh.P_PLAIN}
 
-    def run(self, q, k, v, out):
+    def run(self, q, k, v, out, amax_out=None):
         bgh.run_blockgrid_hip(q, k, v, out, plan=self.plan, f_cur=1, h=1, w=self.lq,
-                              n=q.shape[1], d=q.shape[2])
+                              n=q.shape[1], d=q.shape[2], amax_out=amax_out)
         return out
 
 
@@ -298,7 +298,7 @@ class Block(nn.Module):
         dev, bf = x.device, torch.bfloat16
         f, h, w = geom["grid"]
         amax = geom["amax"]
-        a0, a1 = amax[0:1], amax[1:2]
+        a0, a1, a2 = amax[0:1], amax[1:2], amax[2:3]
         mod = (self.modulation.float() + e).reshape(6, dim).contiguous()
 
         def norm_quant(src, w, b, sc, sh, eps, res=None):
@@ -312,6 +312,13 @@ class Block(nn.Module):
             _lib.ln_modulate_fp8(src, w, b, sc, sh, eps, tq, ts, a0, res_y=res[0],
                                  res_gate=res[1], res_out=xo)
             return xo, tq, ts
+
+        def quant_from(t, word):
+            """e4m3 codes and scale of t, whose amax its producer wrote into word."""
+            tq = torch.empty(t.shape, dtype=FP8_DTYPE, device=dev)
+            ts = torch.empty(1, dtype=torch.float32, device=dev)
+            _lib.fp8_quant_apply(t, tq, ts, word)
+            return tq, ts
 
         # self-attention
         x, xq, xs = norm_quant(x, None, None, mod[1], mod[0], self.norm1.eps, pending)
@@ -328,18 +335,19 @@ class Block(nn.Module):
         att_out = torch.empty(s, n, d, dtype=bf, device=dev)
         if ring is None:
             bgh.run_blockgrid_hip(q.view(s, n, d), k.view(s, n, d), v.view(s, n, d), att_out,
-                                  plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d)
+                                  plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d, amax_out=a2)
         elif geom.get("ring_cat"):
             # the reference's concatenation of the cache with the chunk (tests only)
             lk, lv = ring.logical(0)
             bgh.run_blockgrid_hip(q.view(s, n, d), torch.cat([lk, k.view(s, n, d)]),
                                   torch.cat([lv, v.view(s, n, d)]), att_out, plan=geom["plan"],
-                                  f_cur=f, h=h, w=w, n=n, d=d)
+                                  f_cur=f, h=h, w=w, n=n, d=d, amax_out=a2)
         else:
             bgh.run_blockgrid_hip(q.view(s, n, d), ring.k[0], ring.v[0], att_out,
                                   plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d,
-                                  ring=ring.kernel_ring(), hr_base=ring.A)
-        y = sa.o(att_out.view(s, dim))
+                                  ring=ring.kernel_ring(), hr_base=ring.A, amax_out=a2)
+        # the output projection's quantiser reuses the amax the attention wrote
+        y = sa.o.gemm(*quant_from(att_out.view(s, dim), a2))
 
         # cross-attention
         x1, xq, xs = norm_quant(x, self.norm3.weight, self.norm3.bias, None, None,
@@ -349,8 +357,9 @@ class Block(nn.Module):
         lc = context.shape[0]
         ck, cv = self.cross_kv(context, geom) if cross_kv is None else cross_kv
         c_out = torch.empty(s, n, d, dtype=bf, device=dev)
-        geom["cross"].run(cq.view(s, n, d), ck.view(lc, n, d), cv.view(lc, n, d), c_out)
-        co = ca.o(c_out.view(s, dim))
+        geom["cross"].run(cq.view(s, n, d), ck.view(lc, n, d), cv.view(lc, n, d), c_out,
+                          amax_out=a2)
+        co = ca.o.gemm(*quant_from(c_out.view(s, dim), a2))
 
         # FFN
         x2, xq, xs = norm_quant(x1, None, None, mod[4], mod[3], self.norm2.eps,
@@ -459,7 +468,7 @@ class SRDiT(nn.Module):
                 # (cos, sin) pairs [s, head_dim/2] for the fused RMSNorm + RoPE kernel
                 "rope_cs": torch.view_as_real(rope).reshape(f * h * w, -1).contiguous(),
                 # amax words of the per-tensor quantisers, reused in stream order
-                "amax": torch.zeros(2, dtype=torch.int32, device=device),
+                "amax": torch.zeros(3, dtype=torch.int32, device=device),
                 "amax_ctx": torch.zeros(1, dtype=torch.int32, device=device),
                 "ones": torch.ones(cfg.dim, dtype=torch.float32, device=device)}
 

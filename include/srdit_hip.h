@@ -78,41 +78,45 @@ int srdit_window_attn_grouped_fwd(const void* q, const void* k, const void* v, v
                                   int head_dim, float scale, int dtype, void* stream);
 
 /*
- * Window attention over a streaming KV cache kept in place, forward: the two
- * launches above with the KV frames addressed through a ring.
+ * The two launches above with two additions, ring addressing and the output's
+ * amax; with ring_frames == 0 and amax_out == NULL they are the launches above.
  *
- * Replaces the per-call concatenation of the cached K/V with the chunk's K/V
- * and the tail slice kept as the next cache
+ * Ring: replaces the per-call concatenation of the cached K/V with the chunk's
+ * K/V and the tail slice kept as the next cache
  * (video_refiner/wan/modules/sr_dit/attention.py:1506-1510, :964-974), ahead
  * of the launch that srdit_window_attn_fwd / _grouped_fwd replace.
- *
  * k, v         [kv_tokens, n_heads, head_dim] = hr_base anchor tokens, then
  *              ring_frames ring slots of H*W tokens, then the current chunk's
  *              frames.  Logical KV frame f (the frame index of the params
  *              table) lives in slot (ring_head[0] + f) mod ring_frames for
  *              f < ring_cached, and in frame ring_frames + (f - ring_cached)
  *              otherwise.
- * ring_frames  slots of the ring (>= 1); ring_cached cached frames (<= ring_frames)
+ * ring_frames  slots of the ring (0: the plain layout; ring_head may then be NULL)
+ * ring_cached  cached frames, 0 <= ring_cached <= ring_frames
  * ring_head    device int32, the slot of the oldest cached frame, read by the
  *              kernels at launch (a launch captured in a graph follows the ring
  *              as it advances); a value outside [0, ring_frames) reads as 0.
+ * Amax: amax_out (nullable) is cleared, then receives the fp32 bits of
+ * max |o| over the written outputs (NaN above infinity): the first pass of
+ * the output projection's per-tensor quantiser (fp8_linear.py:80-130), which
+ * srdit_fp8_quant_apply then completes.
  * Other arguments as srdit_window_attn_fwd / srdit_window_attn_grouped_fwd.
  */
-int srdit_window_attn_ring_fwd(const void* q, const void* k, const void* v, void* o,
-                               const int32_t* params, const int32_t* order,
-                               int n_w, int m_tiles, int p_stride, int hr_base,
-                               int H, int W, int64_t q_tokens, int64_t kv_tokens,
-                               int n_heads, int head_dim, float scale, int mode,
-                               int ring_frames, int ring_cached, const int32_t* ring_head,
-                               int dtype, void* stream);
+int srdit_window_attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
+                             const int32_t* params, const int32_t* order,
+                             int n_w, int m_tiles, int p_stride, int hr_base,
+                             int H, int W, int64_t q_tokens, int64_t kv_tokens,
+                             int n_heads, int head_dim, float scale, int mode,
+                             int ring_frames, int ring_cached, const int32_t* ring_head,
+                             uint32_t* amax_out, int dtype, void* stream);
 
-int srdit_window_attn_grouped_ring_fwd(const void* q, const void* k, const void* v, void* o,
-                                       const int32_t* params, const int32_t* groups,
-                                       int n_w, int n_groups, int hr_base, int H, int W,
-                                       int64_t q_tokens, int64_t kv_tokens, int n_heads,
-                                       int head_dim, float scale, int ring_frames,
-                                       int ring_cached, const int32_t* ring_head,
-                                       int dtype, void* stream);
+int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, const void* v, void* o,
+                                     const int32_t* params, const int32_t* groups,
+                                     int n_w, int n_groups, int hr_base, int H, int W,
+                                     int64_t q_tokens, int64_t kv_tokens, int n_heads,
+                                     int head_dim, float scale, int ring_frames,
+                                     int ring_cached, const int32_t* ring_head,
+                                     uint32_t* amax_out, int dtype, void* stream);
 
 /*
  * Row-wise fp8 e4m3 quantiser: for each row of x [M, K] (row stride ldx),

@@ -275,3 +275,34 @@ def test_grouped_kernel_refuses_anchor_plans():
     with pytest.raises(ValueError, match="grouped"):
         bgh.run_blockgrid_hip(q, kv, kv, torch.empty_like(q), plan=plan, f_cur=2, h=8, w=12, n=2,
                               d=128, anchor_mode="chunk", kernel="grouped")
+
+
+@pytest.mark.parametrize("cfg,anchor,kernel", [("c3", None, "auto"), ("c2", None, "single"),
+                                               ("prod", "frame", "auto")])
+def test_output_amax_word(cfg, anchor, kernel):
+    """amax_out receives the fp32 bits of max |out| (the first pass of the output
+    projection's per-tensor quantiser), and asking for it leaves out unchanged."""
+    if cfg == "prod":
+        spec = att._BlockGridSpec(f_cur=3, f_kv=12, h=45, w=80, block_t=3, bh=4, bw=4, rh=3,
+                                  rw=3, rt=3, streaming=True)
+        L = 45 * 80
+        q = _rand((3 * L, 24, 128), 31, 128 ** -0.5).to(DEV)
+        k = _rand((15 * L, 24, 128), 32, 128 ** -0.5).to(DEV)
+        v = _rand((15 * L, 24, 128), 33, 1.0).to(DEV)
+    else:
+        spec = wl.window_spec(cfg)
+        q, k, v, _, _ = wl.make_window_inputs(cfg, torch.bfloat16, DEV, seed=9)
+        q, k, v = q[0].contiguous(), k[0].contiguous(), v[0].contiguous()
+    plan = bgh.build_plan(spec, anchor_mode=anchor)
+    ref = torch.empty_like(q)
+    out = torch.empty_like(q)
+    kw = dict(plan=plan, f_cur=spec.f_cur, h=spec.h, w=spec.w, n=24, d=128, anchor_mode=anchor,
+              kernel=kernel)
+    print(f"[case] amax {cfg} anchor={anchor} kernel={kernel}", flush=True)
+    bgh.run_blockgrid_hip(q, k, v, ref, **kw)
+    word = torch.full((1,), -1, dtype=torch.int32, device=DEV)  # cleared by the launch
+    bgh.run_blockgrid_hip(q, k, v, out, amax_out=word, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    want = out.float().abs().max().view(torch.int32)
+    assert int(word) == int(want)
