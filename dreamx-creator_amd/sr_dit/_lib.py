@@ -49,8 +49,6 @@ SIGNATURES = {
                                              _c_p, _c_p, _c_p]),
     "srdit_ln_modulate": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_f,
                                    _c_p, _c_i64, _c_p, _c_p]),
-    "srdit_ln_modulate_fp8": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_f,
-                                       _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p]),
     "srdit_residual_gate": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_int, _c_i64, _c_i64, _c_p,
                                      _c_i64, _c_p]),
     "srdit_rmsnorm_rope": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_f, _c_p, _c_int, _c_p,
@@ -260,25 +258,6 @@ def ln_modulate(x, ln_w, ln_b, scale, shift, eps, out, amax_ws=None):
                                   _ptr(shift), float(eps), _ptr(out), out.stride(0), _ptr(amax_ws),
                                   _stream(x.device))
     _check(rc, "srdit_ln_modulate")
-
-
-def ln_modulate_fp8(x, ln_w, ln_b, scale, shift, eps, xq, xscale, amax_ws, res_y=None,
-                    res_gate=None, res_out=None):
-    """e4m3 codes ``xq`` [M, K] and scale of bf16(LayerNorm(x) [affine] [modulation]),
-    on x1 = bf16(x + res_y * res_gate) (stored to ``res_out``) when ``res_y`` is given."""
-    _bf16_rows("ln_modulate_fp8 x", x)
-    M, K = x.shape
-    if xq.dtype != torch.float8_e4m3fn or tuple(xq.shape) != (M, K) or not xq.is_contiguous():
-        raise ValueError(f"ln_modulate_fp8: xq must be contiguous float8_e4m3fn [{M}, {K}]")
-    if res_y is not None:
-        _bf16_rows("ln_modulate_fp8 res_y", res_y)
-        _bf16_rows("ln_modulate_fp8 res_out", res_out)
-    rc = load().srdit_ln_modulate_fp8(
-        _ptr(x), M, K, x.stride(0), _ptr(ln_w), _ptr(ln_b), _ptr(scale), _ptr(shift), float(eps),
-        _ptr(res_y), 0 if res_y is None else res_y.stride(0), _ptr(res_gate), _ptr(res_out),
-        0 if res_out is None else res_out.stride(0), _ptr(xq), _ptr(xscale), _ptr(amax_ws),
-        _stream(x.device))
-    _check(rc, "srdit_ln_modulate_fp8")
 
 
 def residual_gate(x, y, gate, out):

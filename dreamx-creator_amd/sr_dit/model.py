@@ -266,8 +266,7 @@ class Block(nn.Module):
         return (x.float() + y.float() * ep[5]).to(dt)
 
 
-    def forward_fused(self, x, e, context, geom, ring=None, cross_kv=None, pending=None,
-                      defer=False):
+    def forward_fused(self, x, e, context, geom, ring=None, cross_kv=None):
         """The same block with the elementwise chains fused into single-pass kernels.
 
         LayerNorm + modulation (+ the amax of its output), RMSNorm + RoPE and
@@ -282,14 +281,8 @@ class Block(nn.Module):
         With a ``ring`` the RMSNorm + RoPE kernel writes K, and the V GEMM
         writes V, straight into the ring's current-chunk region, and the window
         kernel reads the cached frames in place (no concatenation).
-
-        Each "gated residual, LayerNorm, modulation, per-tensor quantiser"
-        chain is one call (``srdit_ln_modulate_fp8``): an amax pass that also
-        stores the new residual stream, then a pass that recomputes the rows
-        and writes the e4m3 codes, so the normalised rows never reach HBM.
-        ``pending`` = (y, gate) is the previous block's FFN residual, applied
-        by this block's first such call; ``defer`` returns this block's own as
-        ``(x2, (y2, gate))`` instead of applying it.
+        The window and cross attention write the amax of their outputs, so the
+        output projections' quantisers need only their quantise pass.
         """
         sa, ca = self.self_attn, self.cross_attn
         cfg = sa.cfg
@@ -301,18 +294,6 @@ class Block(nn.Module):
         a0, a1, a2 = amax[0:1], amax[1:2], amax[2:3]
         mod = (self.modulation.float() + e).reshape(6, dim).contiguous()
 
-        def norm_quant(src, w, b, sc, sh, eps, res=None):
-            """(residual stream, e4m3 codes, scale) of LN(src [+ y * gate]) [* w + b] [mod]."""
-            tq = torch.empty(s, dim, dtype=FP8_DTYPE, device=dev)
-            ts = torch.empty(1, dtype=torch.float32, device=dev)
-            if res is None:
-                _lib.ln_modulate_fp8(src, w, b, sc, sh, eps, tq, ts, a0)
-                return src, tq, ts
-            xo = torch.empty_like(src)
-            _lib.ln_modulate_fp8(src, w, b, sc, sh, eps, tq, ts, a0, res_y=res[0],
-                                 res_gate=res[1], res_out=xo)
-            return xo, tq, ts
-
         def quant_from(t, word):
             """e4m3 codes and scale of t, whose amax its producer wrote into word."""
             tq = torch.empty(t.shape, dtype=FP8_DTYPE, device=dev)
@@ -321,7 +302,9 @@ class Block(nn.Module):
             return tq, ts
 
         # self-attention
-        x, xq, xs = norm_quant(x, None, None, mod[1], mod[0], self.norm1.eps, pending)
+        attn_in = torch.empty(s, dim, dtype=bf, device=dev)
+        _lib.ln_modulate(x, None, None, mod[1], mod[0], self.norm1.eps, attn_in, a0)
+        xq, xs = quant_from(attn_in, a0)
         q_lin, k_lin = sa.q.gemm(xq, xs), sa.k.gemm(xq, xs)
         if ring is None:
             v = sa.v.gemm(xq, xs)
@@ -349,9 +332,12 @@ class Block(nn.Module):
         # the output projection's quantiser reuses the amax the attention wrote
         y = sa.o.gemm(*quant_from(att_out.view(s, dim), a2))
 
+        x1 = apply_residual(x, (y, mod[2]))
+
         # cross-attention
-        x1, xq, xs = norm_quant(x, self.norm3.weight, self.norm3.bias, None, None,
-                                self.norm3.eps, (y, mod[2]))
+        xn = torch.empty_like(x)
+        _lib.ln_modulate(x1, self.norm3.weight, self.norm3.bias, None, None, self.norm3.eps, xn, a0)
+        xq, xs = quant_from(xn, a0)
         cq = torch.empty(s, dim, dtype=bf, device=dev)
         _lib.rmsnorm_rope(ca.q.gemm(xq, xs), ca.norm_q.weight, ca.norm_q.eps, None, d, cq)
         lc = context.shape[0]
@@ -361,16 +347,17 @@ class Block(nn.Module):
                           amax_out=a2)
         co = ca.o.gemm(*quant_from(c_out.view(s, dim), a2))
 
+        x2 = apply_residual(x1, (co, geom["ones"]))
+
         # FFN
-        x2, xq, xs = norm_quant(x1, None, None, mod[4], mod[3], self.norm2.eps,
-                                (co, geom["ones"]))
+        ffn_in = torch.empty_like(x)
+        _lib.ln_modulate(x2, None, None, mod[4], mod[3], self.norm2.eps, ffn_in, a0)
+        xq, xs = quant_from(ffn_in, a0)
         hlin = self.ffn[0].gemm(xq, xs)
         hq = torch.empty(hlin.shape, dtype=FP8_DTYPE, device=dev)
         hs = torch.empty(1, dtype=torch.float32, device=dev)
         _lib.fp8_quant_tensor_gelu(hlin, hq, hs, a1)     # h = GELU in place, amax, quantisation
         y2 = self.ffn[2].gemm(hq, hs)
-        if defer:
-            return x2, (y2, mod[5])
         return apply_residual(x2, (y2, mod[5]))
 
     def cross_kv(self, context, geom):
@@ -486,21 +473,11 @@ class SRDiT(nn.Module):
 
     def blocks_forward(self, x, e0, context, geom, rings=None, cross=None):
         """The 30-block stack: x [s, dim] bf16 -> [s, dim].  ``rings``/``cross``:
-        per-layer streaming KV caches and cached text K/V (or None).  Between
-        fused blocks the FFN's gated residual is applied by the next block's
-        first LayerNorm call instead of a pass of its own."""
-        pending = None
+        per-layer streaming KV caches and cached text K/V (or None)."""
         for i, blk in enumerate(self.blocks):
-            ring = None if rings is None else rings[i]
-            ckv = None if cross is None else cross[i]
-            if FUSED and x.dtype == torch.bfloat16 and blk.fusable():
-                x, pending = blk.forward_fused(x, e0, context, geom, ring=ring, cross_kv=ckv,
-                                               pending=pending, defer=True)
-            else:
-                if pending is not None:
-                    x, pending = apply_residual(x, pending), None
-                x = blk(x, e0, context, geom, ring=ring, cross_kv=ckv)
-        return x if pending is None else apply_residual(x, pending)
+            x = blk(x, e0, context, geom, ring=None if rings is None else rings[i],
+                    cross_kv=None if cross is None else cross[i])
+        return x
 
     def embed_patches(self, latent):
         """The patch-embedding Conv3d (models.py:1551-1552; kernel = stride = patch)

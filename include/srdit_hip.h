@@ -211,25 +211,6 @@ int srdit_ln_modulate(const void* x, int64_t M, int K, int64_t ldx, const void* 
                       void* out, int64_t ldo, uint32_t* amax_ws, void* stream);
 
 /*
- * The same LayerNorm + modulation rows, quantised to e4m3 under their
- * per-tensor scale without being stored: the chain "norm, modulate, then the
- * next Linear's per-tensor quantiser" (models.py:1308 / :1258 into
- * fp8_linear.py:80-130 with one scale), as two passes over x: the first
- * reduces max |out| into amax_ws (cleared first), the second recomputes each
- * row and writes xq [M, K] e4m3 (row stride K) and scale[0] = max(amax *
- * fl32(1/448), 1e-12).  The codes equal srdit_ln_modulate followed by
- * srdit_fp8_quant_apply bit for bit.
- * res_y (nullable): normalise x1 = bf16(x + res_y * res_gate) instead (the
- * gated residual of models.py:1344 / :1260; res_y bf16 [M, K] row stride ldy,
- * res_gate fp32 [K]), storing x1 to res_out (row stride ldr; may be x).
- * K % 8 == 0 (K <= 4096 with a residual), 16-byte rows, xq 8-byte aligned.
- */
-int srdit_ln_modulate_fp8(const void* x, int64_t M, int K, int64_t ldx, const void* ln_w,
-                          const void* ln_b, const float* scale, const float* shift, float eps,
-                          const void* res_y, int64_t ldy, const float* res_gate, void* res_out,
-                          int64_t ldr, void* xq, float* xscale, uint32_t* amax_ws, void* stream);
-
-/*
  * Gated residual: out = bf16(f32(x) + f32(y) * gate[k]) over [M, K] bf16,
  * gate fp32 [K]; out may alias x.  The block's residual updates
  * (models.py:1344, :1260).

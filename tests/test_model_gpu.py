@@ -207,54 +207,6 @@ def test_fused_ln_modulate_and_amax():
                 atol=1e-4 * 2 ** -7)
 
 
-@pytest.mark.parametrize("affine,mod,res,M", [(False, True, False, 700), (True, False, True, 513),
-                                               (False, True, True, 2049), (True, True, True, 64)])
-def test_ln_modulate_fp8_equals_ln_then_quantiser(affine, mod, res, M):
-    """srdit_ln_modulate_fp8 against srdit_ln_modulate + srdit_fp8_quant_apply (and, with a
-    residual, srdit_residual_gate first): bit-identical codes, scale and residual stream."""
-    from sr_dit import _lib
-    g = torch.Generator("cpu").manual_seed(M)
-    K = 3072
-    x = (torch.randn(M, K, generator=g) * 2 + 0.3).to(torch.bfloat16).to(DEV)
-    y = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
-    gate = (torch.randn(K, generator=g) * 0.5).to(DEV)
-    w = (torch.randn(K, generator=g) * 0.5 + 1).to(torch.bfloat16).to(DEV) if affine else None
-    b = (torch.randn(K, generator=g) * 0.1).to(torch.bfloat16).to(DEV) if affine else None
-    sc = (torch.randn(K, generator=g) * 0.1).to(DEV) if mod else None
-    sh = (torch.randn(K, generator=g) * 0.1).to(DEV) if mod else None
-    amax = torch.zeros(1, dtype=torch.int32, device=DEV)
-    # two-step path
-    src = x
-    if res:
-        src = torch.empty_like(x)
-        _lib.residual_gate(x, y, gate, src)
-        assert torch.equal(src, (x.float() + y.float() * gate).to(torch.bfloat16))
-    rows = torch.empty_like(x)
-    _lib.ln_modulate(src, w, b, sc, sh, 1e-6, rows, amax)
-    q_ref = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=DEV)
-    s_ref = torch.empty(1, device=DEV)
-    _lib.fp8_quant_apply(rows, q_ref, s_ref, amax)
-    # one call
-    amax2 = torch.full((1,), 12345, dtype=torch.int32, device=DEV)  # cleared by the call
-    q = torch.empty_like(q_ref)
-    s2 = torch.empty(1, device=DEV)
-    xo = torch.empty_like(x) if res else None
-    _lib.ln_modulate_fp8(x, w, b, sc, sh, 1e-6, q, s2, amax2, res_y=y if res else None,
-                         res_gate=gate if res else None, res_out=xo)
-    torch.cuda.synchronize()
-    print(f"[case] ln_modulate_fp8 affine={affine} mod={mod} res={res} M={M}", flush=True)
-    assert torch.equal(s2, s_ref) and int(amax2) == int(amax)
-    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
-    if res:
-        assert torch.equal(xo, src)
-        # in place: the residual stream overwrites x
-        xi = x.clone()
-        _lib.ln_modulate_fp8(xi, w, b, sc, sh, 1e-6, q, s2, amax2, res_y=y, res_gate=gate,
-                             res_out=xi)
-        torch.cuda.synchronize()
-        assert torch.equal(xi, src) and torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
-
-
 def test_fused_residual_gate_bit_exact():
     from sr_dit import _lib
     g = torch.Generator("cpu").manual_seed(6)
