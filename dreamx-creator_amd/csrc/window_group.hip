@@ -101,8 +101,8 @@ struct FillCursor {
   int blk;       // LDS byte offset of the slot's block within a stage
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
+template <typename T, int D, int MEMBERS>
+__global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a) {
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr int KS = D / 16;      // k-steps of the S^T MFMA over the head dim
@@ -113,12 +113,13 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   constexpr int KPI = 64 / CPK;   // key rows per fill load
   constexpr int BLK = GKN * D;    // elements per block
   constexpr int BLKB = BLK * static_cast<int>(sizeof(T));
-  // [stage][block] rings: 2 stages x 2 blocks x 32 keys x D, for K and for V
-  __shared__ __attribute__((aligned(16))) T ksh[4 * BLK];
-  __shared__ __attribute__((aligned(16))) T vsh[4 * BLK];
+  // [stage][block] rings: 2 stages x MEMBERS blocks x 32 keys x D, for K and for V
+  __shared__ __attribute__((aligned(16))) T ksh[2 * MEMBERS * BLK];
+  __shared__ __attribute__((aligned(16))) T vsh[2 * MEMBERS * BLK];
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int member = wave >> 1, qhalf = wave & 1, kv_role = wave & 1;  // kv_role 0: K, 1: V
+  // kv_role 0: K, 1: V
+  const int member = MEMBERS == 2 ? wave >> 1 : 0, qhalf = wave & 1, kv_role = wave & 1;
   const int lane = threadIdx.x & 63;
   const int c = lane & 31, hf = lane >> 5;
 
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   const int32_t* gp = a.groups + 4 * static_cast<int64_t>(gi);
   int row0 = gp[0], mt0 = gp[1], row1 = gp[2], mt1 = gp[3];
   row0 = row0 < 0 ? 0 : (row0 >= a.n_w ? a.n_w - 1 : row0);
-  row1 = row1 < 0 ? -1 : (row1 >= a.n_w ? a.n_w - 1 : row1);
+  row1 = (MEMBERS == 1 || row1 < 0) ? -1 : (row1 >= a.n_w ? a.n_w - 1 : row1);
   const int32_t* p0 = a.params + static_cast<int64_t>(row0) * 19;
   const int32_t* p1 = row1 >= 0 ? a.params + static_cast<int64_t>(row1) * 19 : p0;
 
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
       int t = cur.row < kh_l ? __mul24(cur.row, a.W) + cur.col : last_tok;
       t += cur.fbase;
       t = static_cast<int>(min(static_cast<uint32_t>(t), static_cast<uint32_t>(kv_tokens - 1)));
-      const uint32_t dst = lds_fill_base + static_cast<uint32_t>(stage * 2 * BLKB + cur.blk);
+      const uint32_t dst = lds_fill_base + static_cast<uint32_t>(stage * MEMBERS * BLKB + cur.blk);
       static_for<NL>([&](auto qc) __attribute__((always_inline)) {
         constexpr int q = decltype(qc)::value;
         int tq = __builtin_amdgcn_mov_dpp(t, 0x150 + q, 0xf, 0xf, false);
@@ -308,7 +309,7 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   struct VOps { V8 t[2][DT]; };
   auto read_k = [&](auto stage_c) __attribute__((always_inline)) -> KOps {
     constexpr int stage = decltype(stage_c)::value;
-    const char* kb = reinterpret_cast<const char*>(ksh) + stage * 2 * BLKB;
+    const char* kb = reinterpret_cast<const char*>(ksh) + stage * MEMBERS * BLKB;
     KOps r;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) r.f[ks] = *reinterpret_cast<const V8*>(kb + ka[ks]);
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
   };
   auto read_v = [&](auto stage_c) __attribute__((always_inline)) -> VOps {
     constexpr int stage = decltype(stage_c)::value;
-    const char* vb = reinterpret_cast<const char*>(vsh) + stage * 2 * BLKB;
+    const char* vb = reinterpret_cast<const char*>(vsh) + stage * MEMBERS * BLKB;
     VOps r;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
@@ -517,12 +518,15 @@ __global__ __launch_bounds__(256) void window_group_kernel(GroupArgs a) {
 __global__ void clear_amax_kernel(uint32_t* p) { *p = 0u; }
 
 template <typename T, int D>
-int launch_group(const GroupArgs& a, uint32_t grid, hipStream_t stream) {
+int launch_group(const GroupArgs& a, int members, uint32_t grid, hipStream_t stream) {
   if (a.amax_out) {
     hipLaunchKernelGGL(clear_amax_kernel, dim3(1), dim3(1), 0, stream, a.amax_out);
     SRDIT_LAUNCH_CHECK("clear_amax_kernel");
   }
-  hipLaunchKernelGGL((window_group_kernel<T, D>), dim3(grid), dim3(256), 0, stream, a);
+  if (members == 1)
+    hipLaunchKernelGGL((window_group_kernel<T, D, 1>), dim3(grid), dim3(128), 0, stream, a);
+  else
+    hipLaunchKernelGGL((window_group_kernel<T, D, 2>), dim3(grid), dim3(256), 0, stream, a);
   SRDIT_LAUNCH_CHECK("window_group_kernel");
   return SRDIT_OK;
 }
@@ -537,7 +541,7 @@ int group_entry(const char* fn, const void* q, const void* k, const void* v, voi
                 const int32_t* params, const int32_t* groups, int n_w, int n_groups, int hr_base,
                 int H, int W, int64_t q_tokens, int64_t kv_tokens, int n_heads, int head_dim,
                 float scale, int ring_R, int ring_nc, const int32_t* ring_head,
-                uint32_t* amax_out, int dtype, void* stream) {
+                uint32_t* amax_out, int members, int dtype, void* stream) {
   SRDIT_REQUIRE(q && k && v && o && params && groups, "%s: null pointer", fn);
   SRDIT_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
                 "%s: q/k/v/o must be 16-byte aligned", fn);
@@ -572,9 +576,12 @@ int group_entry(const char* fn, const void* q, const void* k, const void* v, voi
   a.ring_R = ring_R; a.ring_nc = ring_nc; a.ring_head = ring_head; a.amax_out = amax_out;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint32_t grid = static_cast<uint32_t>(grid64);
+  SRDIT_REQUIRE(members == 1 || members == 2, "%s: members must be 1 or 2, got %d", fn, members);
   if (dtype == SRDIT_DTYPE_BF16)
-    return head_dim == 128 ? launch_group<__bf16, 128>(a, grid, s) : launch_group<__bf16, 64>(a, grid, s);
-  return head_dim == 128 ? launch_group<_Float16, 128>(a, grid, s) : launch_group<_Float16, 64>(a, grid, s);
+    return head_dim == 128 ? launch_group<__bf16, 128>(a, members, grid, s)
+                           : launch_group<__bf16, 64>(a, members, grid, s);
+  return head_dim == 128 ? launch_group<_Float16, 128>(a, members, grid, s)
+                         : launch_group<_Float16, 64>(a, members, grid, s);
 }
 
 }  // namespace
@@ -587,7 +594,7 @@ extern "C" int srdit_window_attn_grouped_fwd(const void* q, const void* k, const
                                              int head_dim, float scale, int dtype, void* stream) {
   return srdit::group_entry("srdit_window_attn_grouped_fwd", q, k, v, o, params, groups, n_w,
                             n_groups, hr_base, H, W, q_tokens, kv_tokens, n_heads, head_dim,
-                            scale, 0, 0, nullptr, nullptr, dtype, stream);
+                            scale, 0, 0, nullptr, nullptr, 2, dtype, stream);
 }
 
 extern "C" int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, const void* v,
@@ -597,7 +604,7 @@ extern "C" int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, co
                                                 int64_t kv_tokens, int n_heads, int head_dim,
                                                 float scale, int ring_frames, int ring_cached,
                                                 const int32_t* ring_head, uint32_t* amax_out,
-                                                int dtype, void* stream) {
+                                                int members, int dtype, void* stream) {
   using namespace srdit;
   const char* fn = "srdit_window_attn_grouped_fwd_ex";
   if (ring_frames != 0) {
@@ -612,5 +619,5 @@ extern "C" int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, co
   }
   return group_entry(fn, q, k, v, o, params, groups, n_w, n_groups, hr_base, H, W, q_tokens,
                      kv_tokens, n_heads, head_dim, scale, ring_frames, ring_cached, ring_head,
-                     amax_out, dtype, stream);
+                     amax_out, members, dtype, stream);
 }

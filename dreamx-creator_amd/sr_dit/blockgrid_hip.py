@@ -219,6 +219,35 @@ def build_groups(plan) -> torch.Tensor:
     return torch.tensor(groups, dtype=torch.int32).reshape(-1, 4).contiguous()
 
 
+def build_singles(plan) -> torch.Tensor:
+    """Every 64-query member alone, in row order: int32 [G, 4] rows (row, m-tile, -1, 0)
+    for the one-member-per-workgroup form of the grouped kernel."""
+    p = plan["params"].tolist()
+    rows = []
+    for r, row in enumerate(p):
+        lq = row[1] * row[4] * row[5]
+        for mt in range(-(-lq // HIP_BLOCK_M) if lq > 0 else 0):
+            rows.append((r, mt, -1, 0))
+    return torch.tensor(rows, dtype=torch.int32).reshape(-1, 4).contiguous()
+
+
+def shared_fraction(plan, groups: torch.Tensor) -> float:
+    """Fraction of the members' KV frames that a pair fetches once for both
+    (2 * shared frames / frames of both members, summed over the table): 1.0
+    when every pair is the two m-tiles of one window, ~2/3 for pairs of
+    neighbouring query frames under a +-1-frame rule, 0 without pairs."""
+    p = plan["params"].tolist()
+    shared = total = 0
+    for r0, _, r1, _ in groups.tolist():
+        a0, la = p[r0][6], p[r0][7]
+        total += la
+        if r1 >= 0:
+            a1, lb = p[r1][6], p[r1][7]
+            total += lb
+            shared += 2 * max(0, min(a0 + la, a1 + lb) - max(a0, a1))
+    return shared / total if total else 0.0
+
+
 def paired_fraction(groups: torch.Tensor) -> float:
     """Fraction of members that share a workgroup with a partner."""
     n = groups.shape[0]
@@ -250,11 +279,15 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     stride-1 head dim, on one device, bf16 or fp16.  The launch is
     asynchronous on the current stream.
 
-    ``kernel``: ``"auto"`` runs plain plans without an anchor prefix whose
-    64-query members pair well (>= 75% paired) on the grouped kernel (two
-    members per workgroup sharing their K/V fetches) and everything else on
-    the single-window kernel; ``"grouped"`` / ``"single"`` force one (a forced
-    grouped launch of an anchored plan raises).
+    ``kernel``: ``"auto"`` runs plain plans without an anchor prefix on the
+    grouped kernel: with two members per workgroup sharing their K/V fetches
+    (``"grouped"``) when the pairs share nearly all their KV frames (the two
+    m-tiles of one window), else with one member per workgroup (``"solo"``);
+    anchored plans and windows of more than 16 KV frames go to the
+    single-window kernel (``"single"``).  Measured on one MI355X: c2 and c3
+    (neighbouring-frame pairs sharing 2 of 3 frames) and the 48-query shipped
+    windows run fastest solo, c4 (m-tile pairs) grouped.  Any of the three
+    can be forced (a forced grouped or solo launch of an anchored plan raises).
 
     ``ring`` = ``(ring_frames, ring_cached, head)``: the HR KV after the anchor
     prefix is an in-place cache (``sr_dit.kv_ring.KVRing``): ``ring_frames``
@@ -286,10 +319,21 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     mode = 1 if anchor_mode == "frame" else 0
     if (plan["p_stride"] == P_FRAME) != (mode == 1):
         raise ValueError("run_blockgrid_hip: plan layout does not match anchor_mode.")
-    if kernel not in ("auto", "grouped", "single"):
-        raise ValueError(f"run_blockgrid_hip: kernel must be auto, grouped or single, got {kernel!r}")
-    if kernel == "grouped" and not groups_supported(plan):
+    if kernel not in ("auto", "grouped", "solo", "single"):
+        raise ValueError("run_blockgrid_hip: kernel must be auto, grouped, solo or single, got "
+                         f"{kernel!r}")
+    if kernel in ("grouped", "solo") and not groups_supported(plan):
         raise ValueError("run_blockgrid_hip: the grouped kernel needs plain rows without an anchor.")
+    if kernel == "solo":
+        key = ("singles", q.device)
+        singles = plan.get(key)
+        if singles is None:
+            singles = plan[key] = build_singles(plan).to(q.device)
+        _lib.window_attn_grouped_fwd(
+            q, k_ext, v_ext, out, params, singles, n_w=plan["n_w"], n_groups=singles.shape[0],
+            hr_base=hr_base, H=h, W=w, n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0],
+            scale=d ** -0.5, ring=ring, amax_out=amax_out, members=1)
+        return out
     use_grouped = False
     if kernel != "single" and groups_supported(plan):
         key = ("groups", q.device)
@@ -297,10 +341,16 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
         if groups is None:
             host = build_groups(plan)
             plan["groups_paired_fraction"] = paired_fraction(host)
+            plan["groups_shared_fraction"] = shared_fraction(plan, host)
             groups = plan[key] = host.to(q.device)
-        # An unpaired member leaves two of its workgroup's four wavefronts
-        # idle; plans that pair poorly run faster on the single-window kernel.
-        use_grouped = kernel == "grouped" or plan["groups_paired_fraction"] >= 0.75
+        # Pairs that share only part of their KV frames, and unpaired members,
+        # run faster one member per workgroup.
+        use_grouped = kernel == "grouped" or (plan["groups_paired_fraction"] >= 0.75 and
+                                              plan["groups_shared_fraction"] >= 0.9)
+        if not use_grouped:
+            return run_blockgrid_hip(q, k_ext, v_ext, out, plan=plan, f_cur=f_cur, h=h, w=w, n=n,
+                                     d=d, anchor_mode=anchor_mode, kernel="solo", ring=ring,
+                                     hr_base=hr_base, amax_out=amax_out)
     if use_grouped:
         _lib.window_attn_grouped_fwd(
             q, k_ext, v_ext, out, params, groups, n_w=plan["n_w"], n_groups=groups.shape[0],

@@ -100,6 +100,10 @@ int srdit_window_attn_grouped_fwd(const void* q, const void* k, const void* v, v
  * max |o| over the written outputs (NaN above infinity): the first pass of
  * the output projection's per-tensor quantiser (fp8_linear.py:80-130), which
  * srdit_fp8_quant_apply then completes.
+ * members (grouped only): 2 runs the grouped launch above (two 64-query
+ * members per workgroup of four wavefronts); 1 runs one member per workgroup
+ * of two wavefronts (row1 of the groups table is ignored), for tables whose
+ * members do not pair.
  * Other arguments as srdit_window_attn_fwd / srdit_window_attn_grouped_fwd.
  */
 int srdit_window_attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
@@ -116,7 +120,7 @@ int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, const void* v
                                      int64_t q_tokens, int64_t kv_tokens, int n_heads,
                                      int head_dim, float scale, int ring_frames,
                                      int ring_cached, const int32_t* ring_head,
-                                     uint32_t* amax_out, int dtype, void* stream);
+                                     uint32_t* amax_out, int members, int dtype, void* stream);
 
 /*
  * Row-wise fp8 e4m3 quantiser: for each row of x [M, K] (row stride ldx),

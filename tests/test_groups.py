@@ -95,3 +95,22 @@ def test_unsupported_plans_and_kernel_switch():
     plan = bgh.build_plan(spec, anchor_mode="chunk")
     assert not bgh.groups_supported(plan)
     assert bgh.groups_supported(bgh.build_plan(spec))
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2", "c3", "c4"])
+def test_singles_cover_every_member_once(cfg):
+    plan = bgh.build_plan(wl.window_spec(cfg))
+    s = bgh.build_singles(plan).tolist()
+    assert all(r1 == -1 for _, _, r1, _ in s)
+    seen = [(r, m) for r, m, _, _ in s]
+    assert len(seen) == len(set(seen)) and set(seen) == _members(plan)
+
+
+def test_shared_fraction_separates_mtile_pairs_from_frame_pairs():
+    """m-tile pairs (c4) share every KV frame; +-1-frame neighbour pairs (c3) share
+    2 of 3 interior frames (2 of 2 / 3 at the clip edges): 0.75 overall."""
+    c3 = bgh.build_plan(wl.window_spec("c3"))
+    c4 = bgh.build_plan(wl.window_spec("c4"))
+    assert bgh.shared_fraction(c4, bgh.build_groups(c4)) == 1.0
+    assert bgh.shared_fraction(c3, bgh.build_groups(c3)) == 0.75
+    assert bgh.shared_fraction(c3, bgh.build_singles(c3)) == 0.0

@@ -3,10 +3,11 @@
 The ring only changes where the kernels fetch each logical KV frame, so every
 output must be bit-identical to the same op on the reference's concatenated
 cache (``pre_cache_k``/``pre_cache_v`` + ``kv_len``, attention.py:1506-1510,
-:964-974) over chunk sequences that wrap the ring.  Covered: both kernels
-(grouped for two-m-tile windows, single-window otherwise), the per-frame and
-whole-chunk LQ anchor, the shipped 4x4/r3 geometry, and a launch captured in a
-HIP graph that keeps following the ring as it advances.
+:964-974) over chunk sequences that wrap the ring.  Covered: the grouped
+kernel with two members per workgroup (two-m-tile windows) and with one (the
+other plain plans), the single-window kernel (the anchored plans), the
+per-frame and whole-chunk LQ anchor, the shipped 4x4/r3 geometry, and a launch
+captured in a HIP graph that keeps following the ring as it advances.
 """
 import pytest
 import torch
@@ -69,8 +70,9 @@ def test_ring_grouped_kernel_two_frame_chunks():
     assert ring.head != 0
 
 
-def test_ring_single_kernel_three_frame_chunks():
-    """3-frame chunks (three m-tiles: single-window kernel), ragged 45x80-style edges."""
+def test_ring_solo_kernel_three_frame_chunks():
+    """3-frame chunks (three m-tiles that do not all pair: one member per workgroup),
+    ragged 45x80-style edges."""
     _stream(21, 36, 3, 4, (8, 8), (1, 1), chunks=7, seed=100)
 
 
@@ -84,7 +86,7 @@ def test_ring_production_geometry():
     _stream(45, 80, 3, 9, (4, 4), (3, 3), chunks=5, anchor="frame", seed=300)
 
 
-@pytest.mark.parametrize("kernel", ["single", "grouped"])
+@pytest.mark.parametrize("kernel", ["single", "grouped", "solo"])
 def test_ring_launcher_both_kernels(kernel):
     """Launcher level: a full ring (head mid-way) against the same frames concatenated."""
     h, w, f_cur, R = 24, 40, 2, 5

@@ -228,9 +228,10 @@ KERNEL_CASES = [c for c in SMALL if c[2] is None]
 
 
 @pytest.mark.parametrize("name,spec,mode", KERNEL_CASES, ids=[c[0] for c in KERNEL_CASES])
-@pytest.mark.parametrize("kernel", ["single", "grouped"])
+@pytest.mark.parametrize("kernel", ["single", "grouped", "solo"])
 def test_both_kernels_vs_float64_oracle(name, spec, mode, kernel):
-    """The single-window and the grouped kernel each against the oracle, peaky inputs."""
+    """The single-window kernel and the grouped kernel (two members or one per
+    workgroup) each against the oracle, peaky inputs."""
     n, d = 4, 128
     g = _geom_of(spec)
     L = spec.h * spec.w
@@ -249,9 +250,10 @@ def test_both_kernels_vs_float64_oracle(name, spec, mode, kernel):
     check_attention(out, ref, label=f"{name}/{kernel}")
 
 
-@pytest.mark.parametrize("cfg", ["c3", "c4"])
-def test_single_kernel_on_benchmark_configs(cfg):
-    """The single-window kernel stays correct on the benchmark sizes the grouped one now runs."""
+@pytest.mark.parametrize("cfg,kernel", [("c3", "single"), ("c4", "single"), ("c3", "grouped"),
+                                        ("c4", "solo")])
+def test_forced_kernels_on_benchmark_configs(cfg, kernel):
+    """Each kernel stays correct on the benchmark sizes where "auto" picks another one."""
     spec = wl.window_spec(cfg)
     q, k, v, kc, vc = wl.make_window_inputs(cfg, torch.bfloat16, DEV, seed=1, temperature=8.0)
     q, k, v = q[0].contiguous(), k[0], v[0]
@@ -261,9 +263,9 @@ def test_single_kernel_on_benchmark_configs(cfg):
     plan = bgh.build_plan(spec)
     out = torch.empty_like(q)
     bgh.run_blockgrid_hip(q, k, v, out, plan=plan, f_cur=spec.f_cur, h=spec.h, w=spec.w,
-                          n=wl.N_HEADS, d=wl.HEAD_DIM, kernel="single")
+                          n=wl.N_HEADS, d=wl.HEAD_DIM, kernel=kernel)
     torch.cuda.synchronize()
-    check_attention(out, _gather_ref(spec, None, q, k, v), label=f"{cfg}/single")
+    check_attention(out, _gather_ref(spec, None, q, k, v), label=f"{cfg}/{kernel}")
 
 
 def test_grouped_kernel_refuses_anchor_plans():
@@ -272,13 +274,14 @@ def test_grouped_kernel_refuses_anchor_plans():
     plan = bgh.build_plan(spec, anchor_mode="chunk")
     q = torch.zeros(2 * 96, 2, 128, dtype=torch.bfloat16, device=DEV)
     kv = torch.zeros(2 * 96 + 4 * 96, 2, 128, dtype=torch.bfloat16, device=DEV)
-    with pytest.raises(ValueError, match="grouped"):
-        bgh.run_blockgrid_hip(q, kv, kv, torch.empty_like(q), plan=plan, f_cur=2, h=8, w=12, n=2,
-                              d=128, anchor_mode="chunk", kernel="grouped")
+    for kernel in ("grouped", "solo"):
+        with pytest.raises(ValueError, match="grouped"):
+            bgh.run_blockgrid_hip(q, kv, kv, torch.empty_like(q), plan=plan, f_cur=2, h=8, w=12,
+                                  n=2, d=128, anchor_mode="chunk", kernel=kernel)
 
 
 @pytest.mark.parametrize("cfg,anchor,kernel", [("c3", None, "auto"), ("c2", None, "single"),
-                                               ("prod", "frame", "auto")])
+                                               ("c4", None, "grouped"), ("prod", "frame", "auto")])
 def test_output_amax_word(cfg, anchor, kernel):
     """amax_out receives the fp32 bits of max |out| (the first pass of the output
     projection's per-tensor quantiser), and asking for it leaves out unchanged."""
