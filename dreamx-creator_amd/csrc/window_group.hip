@@ -1,6 +1,6 @@
 // Grouped block-grid window attention forward for gfx950 (MI355X): plain-mode
 // windows without an anchor prefix, two 64-query members per workgroup that
-// share their K/V fetches.
+// share their K/V fetches, or one member per workgroup (MEMBERS = 1).
 //
 // A member is one 64-query tile of one window (a params row and an m-tile).
 // The host pairs members whose KV cuboids have the same spatial extent: the
@@ -15,9 +15,15 @@
 // step, one per member), then the shared frames, whose blocks are fetched
 // once and consumed by both members.  For the +-1-frame rule this cuts the
 // L2->LDS fill traffic of a pair of neighbouring query frames from 5 or 6
-// frames to 3 or 4.  Fills of step i+1 go to the other half of a two-stage
-// ring while step i computes; in a private slot wavefronts 2m (K) and 2m+1 (V)
-// fetch member m's block, in a shared slot wavefronts 0 (K) and 1 (V) fetch it.
+// frames to 3 or 4.  Fills run ahead into rings (K two stages, two steps
+// ahead; V two stages one step ahead, or three stages two steps ahead in the
+// one-member form) while the current step computes; in a private slot
+// wavefronts 2m (K) and 2m+1 (V) fetch member m's block, in a shared slot
+// wavefronts 0 (K) and 1 (V) fetch it.
+//
+// The one-member form (two wavefronts, 40 KB of LDS, four workgroups per CU)
+// runs faster than pairs that share only part of their frames; pairs of the
+// two m-tiles of one window (identical KV) run faster in the two-member form.
 //
 // Numerics are those of the plain kernel (blockgrid_triton.py:184-278): fp32
 // scores scaled by d^-1/2, masked keys never contribute, P rounded to the
@@ -115,7 +121,10 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   constexpr int BLKB = BLK * static_cast<int>(sizeof(T));
   // [stage][block] rings: 2 stages x MEMBERS blocks x 32 keys x D, for K and for V
   __shared__ __attribute__((aligned(16))) T ksh[2 * MEMBERS * BLK];
-  __shared__ __attribute__((aligned(16))) T vsh[2 * MEMBERS * BLK];
+  // The one-member form has LDS to spare (four workgroups per CU at 40 KB):
+  // its V ring has three stages and V is fetched two steps ahead, as K is.
+  constexpr int VST = MEMBERS == 1 ? 3 : 2;
+  __shared__ __attribute__((aligned(16))) T vsh[VST * MEMBERS * BLK];
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // kv_role 0: K, 1: V
@@ -226,10 +235,11 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   }
 
   // ---- fills ----------------------------------------------------------------
-  // Step t goes to stage t & 1.  In a private step block b holds member b's
-  // keys and is fetched by wavefronts 2b (K) and 2b+1 (V); in a shared step
-  // block 0 is fetched by wavefronts 0 and 1.  K is fetched two steps ahead of
-  // its use, V one step ahead.  Source lane s of a 16-lane row decodes the
+  // Step t goes to K stage t % 2 and V stage t % VST.  In a private step block
+  // b holds member b's keys and is fetched by wavefronts 2b (K) and 2b+1 (V);
+  // in a shared step block 0 is fetched by wavefronts 0 and 1.  K is fetched
+  // two steps ahead of its use, V one (VST 2) or two (VST 3) steps ahead.
+  // Source lane s of a 16-lane row decodes the
   // token of the key that load (s % LPK) places in that row; DPP row_newbcast
   // hands it to the row.
   const int s16 = lane & 15;
@@ -256,7 +266,7 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   };
   cur.fs = 0; cur.s = 0; cur.row = row_start; cur.col = col_start;
   cursor_slot();
-  const int look = kv_role == 0 ? 2 : 1;  // steps ahead this wavefront fetches
+  const int look = (kv_role == 0 || VST == 3) ? 2 : 1;  // steps ahead this wavefront fetches
   // Fetch the cursor's step into stage `stage` and advance.
   auto fill_next = [&](int stage) __attribute__((always_inline)) {
     if (__builtin_expect(cur.part, 1)) {  // uniform
@@ -411,7 +421,7 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   // Prologue: K of steps 0 and 1, V of step 0; S^T of step 0.
   if (nsteps > 0) {
     fill_next(0);
-    if (kv_role == 0 && nsteps > 1) fill_next(1);
+    if ((kv_role == 0 || VST == 3) && nsteps > 1) fill_next(1);
   }
   fill_barrier();
   f32x16_t s_cur = f32x16_t{};
@@ -420,11 +430,18 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   int fs = 0, s = 0;  // frame slot and spatial step of step j
   bool do_pv = nsteps > 0 && active(0);  // the member consumes step j
   const int tail_valid = sp - (nS - 1) * GKN;  // keys of a frame's last block
-  auto iteration = [&](int j, auto stage_c) __attribute__((always_inline)) {
-    constexpr int stage = decltype(stage_c)::value;  // stage of step j
+  auto iteration = [&](int j, auto stage_c, auto vstage_c) __attribute__((always_inline)) {
+    constexpr int stage = decltype(stage_c)::value;    // K stage of step j: j % 2
+    constexpr int vstage = decltype(vstage_c)::value;  // V stage of step j: j % VST
     fill_barrier();  // K of j+1 and V of j landed; iteration j-1's LDS reads retired everywhere
-    // K: step j+2 into stage j&1; V: step j+1 into stage (j+1)&1.
-    if (j + look < nsteps) fill_next(stage ^ (look & 1));
+    // K: step j+2 into stage j % 2; V: step j+2 into stage (j+2) % 3 (three
+    // stages) or step j+1 into stage (j+1) % 2.  Those stages were last read
+    // in iteration j-1, which every wavefront has finished.
+    if (j + look < nsteps) {
+      if (kv_role == 0) fill_next(stage);
+      else if (VST == 3) fill_next((vstage + 2) % 3);
+      else fill_next(stage ^ 1);
+    }
     // private -> shared: the K block of step j+1 and the V block of step j
     // move to block 0 (once each; member 1 only)
     if (__builtin_expect(j + 1 == first_shared && member == 1, 0)) {
@@ -442,7 +459,7 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
     f32x16_t s_next;
     if (__builtin_expect(do_pv, 1)) {  // uniform
       if (__builtin_expect(s == nS - 1 && tail_valid < GKN, 0)) mask_tail(s_cur, tail_valid);
-      const VOps vt = read_v(std::integral_constant<int, stage>{});
+      const VOps vt = read_v(std::integral_constant<int, vstage>{});
       if (__builtin_expect(!minit, 0)) {  // first active block: m = its row max
         mrun = row_max(s_cur);
         shift(s_cur, mrun);
@@ -486,12 +503,33 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
       do_pv = active(fs);
     }
   };
+  // Unrolled so that both ring stages are immediates: by 2, or by 6 with a
+  // three-stage V ring.
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
   int j = 0;
-  for (; j + 1 < nsteps; j += 2) {
-    iteration(j, std::integral_constant<int, 0>{});
-    iteration(j + 1, std::integral_constant<int, 1>{});
+  if constexpr (VST == 3) {
+    for (; j + 5 < nsteps; j += 6) {
+      iteration(j, I0{}, I0{});
+      iteration(j + 1, I1{}, I1{});
+      iteration(j + 2, I0{}, I2{});
+      iteration(j + 3, I1{}, I0{});
+      iteration(j + 4, I0{}, I1{});
+      iteration(j + 5, I1{}, I2{});
+    }
+    if (j < nsteps) iteration(j, I0{}, I0{});  // j % 6 == 0 here
+    if (j + 1 < nsteps) iteration(j + 1, I1{}, I1{});
+    if (j + 2 < nsteps) iteration(j + 2, I0{}, I2{});
+    if (j + 3 < nsteps) iteration(j + 3, I1{}, I0{});
+    if (j + 4 < nsteps) iteration(j + 4, I0{}, I1{});
+  } else {
+    for (; j + 1 < nsteps; j += 2) {
+      iteration(j, I0{}, I0{});
+      iteration(j + 1, I1{}, I1{});
+    }
+    if (j < nsteps) iteration(j, I0{}, I0{});
   }
-  if (j < nsteps) iteration(j, std::integral_constant<int, 0>{});
 
   // O = acc / l ; lane (c, hf) writes dims dt*32 + 8*g4 + 4*hf + [0, 4) of its query
   const float lt = half_sum(lrun);
