@@ -15,9 +15,8 @@
 // step, one per member), then the shared frames, whose blocks are fetched
 // once and consumed by both members.  For the +-1-frame rule this cuts the
 // L2->LDS fill traffic of a pair of neighbouring query frames from 5 or 6
-// frames to 3 or 4.  Fills run ahead into rings (K two stages, two steps
-// ahead; V two stages one step ahead, or three stages two steps ahead in the
-// one-member form) while the current step computes; in a private slot
+// frames to 3 or 4.  Fills run two steps ahead into rings (K two stages, V
+// three) while the current step computes; in a private slot
 // wavefronts 2m (K) and 2m+1 (V) fetch member m's block, in a shared slot
 // wavefronts 0 (K) and 1 (V) fetch it.
 //
@@ -121,9 +120,10 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   constexpr int BLKB = BLK * static_cast<int>(sizeof(T));
   // [stage][block] rings: 2 stages x MEMBERS blocks x 32 keys x D, for K and for V
   __shared__ __attribute__((aligned(16))) T ksh[2 * MEMBERS * BLK];
-  // The one-member form has LDS to spare (four workgroups per CU at 40 KB):
-  // its V ring has three stages and V is fetched two steps ahead, as K is.
-  constexpr int VST = MEMBERS == 1 ? 3 : 2;
+  // The V ring has three stages and V is fetched two steps ahead, as K is:
+  // 40 KB per member, so the one-member form still fits four workgroups and
+  // the two-member form two workgroups in a CU's 160 KB.
+  constexpr int VST = 3;
   __shared__ __attribute__((aligned(16))) T vsh[VST * MEMBERS * BLK];
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -237,8 +237,8 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   // ---- fills ----------------------------------------------------------------
   // Step t goes to K stage t % 2 and V stage t % VST.  In a private step block
   // b holds member b's keys and is fetched by wavefronts 2b (K) and 2b+1 (V);
-  // in a shared step block 0 is fetched by wavefronts 0 and 1.  K is fetched
-  // two steps ahead of its use, V one (VST 2) or two (VST 3) steps ahead.
+  // in a shared step block 0 is fetched by wavefronts 0 and 1.  K and V are
+  // fetched two steps ahead of their use.
   // Source lane s of a 16-lane row decodes the
   // token of the key that load (s % LPK) places in that row; DPP row_newbcast
   // hands it to the row.
@@ -266,7 +266,7 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   };
   cur.fs = 0; cur.s = 0; cur.row = row_start; cur.col = col_start;
   cursor_slot();
-  const int look = (kv_role == 0 || VST == 3) ? 2 : 1;  // steps ahead this wavefront fetches
+  constexpr int look = 2;  // steps ahead the fills run
   // Fetch the cursor's step into stage `stage` and advance.
   auto fill_next = [&](int stage) __attribute__((always_inline)) {
     if (__builtin_expect(cur.part, 1)) {  // uniform
@@ -418,10 +418,10 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
     for (int dt = 0; dt < DT; ++dt) oacc[dt] = E::mma(vt.t[1][dt], pb, oacc[dt]);
   };
 
-  // Prologue: K of steps 0 and 1, V of step 0; S^T of step 0.
+  // Prologue: K and V of steps 0 and 1; S^T of step 0.
   if (nsteps > 0) {
     fill_next(0);
-    if ((kv_role == 0 || VST == 3) && nsteps > 1) fill_next(1);
+    if (nsteps > 1) fill_next(1);
   }
   fill_barrier();
   f32x16_t s_cur = f32x16_t{};
@@ -434,14 +434,9 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
     constexpr int stage = decltype(stage_c)::value;    // K stage of step j: j % 2
     constexpr int vstage = decltype(vstage_c)::value;  // V stage of step j: j % VST
     fill_barrier();  // K of j+1 and V of j landed; iteration j-1's LDS reads retired everywhere
-    // K: step j+2 into stage j % 2; V: step j+2 into stage (j+2) % 3 (three
-    // stages) or step j+1 into stage (j+1) % 2.  Those stages were last read
-    // in iteration j-1, which every wavefront has finished.
-    if (j + look < nsteps) {
-      if (kv_role == 0) fill_next(stage);
-      else if (VST == 3) fill_next((vstage + 2) % 3);
-      else fill_next(stage ^ 1);
-    }
+    // Step j+2: K into stage j % 2, V into stage (j+2) % 3.  Both were last
+    // read in iteration j-1, which every wavefront has finished.
+    if (j + look < nsteps) fill_next(kv_role == 0 ? stage : (vstage + 2) % VST);
     // private -> shared: the K block of step j+1 and the V block of step j
     // move to block 0 (once each; member 1 only)
     if (__builtin_expect(j + 1 == first_shared && member == 1, 0)) {
@@ -503,33 +498,25 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
       do_pv = active(fs);
     }
   };
-  // Unrolled so that both ring stages are immediates: by 2, or by 6 with a
-  // three-stage V ring.
+  // Unrolled by 6 so that both ring stages (j % 2, j % 3) are immediates.
+  static_assert(VST == 3, "the unrolling below assumes a three-stage V ring");
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   int j = 0;
-  if constexpr (VST == 3) {
-    for (; j + 5 < nsteps; j += 6) {
-      iteration(j, I0{}, I0{});
-      iteration(j + 1, I1{}, I1{});
-      iteration(j + 2, I0{}, I2{});
-      iteration(j + 3, I1{}, I0{});
-      iteration(j + 4, I0{}, I1{});
-      iteration(j + 5, I1{}, I2{});
-    }
-    if (j < nsteps) iteration(j, I0{}, I0{});  // j % 6 == 0 here
-    if (j + 1 < nsteps) iteration(j + 1, I1{}, I1{});
-    if (j + 2 < nsteps) iteration(j + 2, I0{}, I2{});
-    if (j + 3 < nsteps) iteration(j + 3, I1{}, I0{});
-    if (j + 4 < nsteps) iteration(j + 4, I0{}, I1{});
-  } else {
-    for (; j + 1 < nsteps; j += 2) {
-      iteration(j, I0{}, I0{});
-      iteration(j + 1, I1{}, I1{});
-    }
-    if (j < nsteps) iteration(j, I0{}, I0{});
+  for (; j + 5 < nsteps; j += 6) {
+    iteration(j, I0{}, I0{});
+    iteration(j + 1, I1{}, I1{});
+    iteration(j + 2, I0{}, I2{});
+    iteration(j + 3, I1{}, I0{});
+    iteration(j + 4, I0{}, I1{});
+    iteration(j + 5, I1{}, I2{});
   }
+  if (j < nsteps) iteration(j, I0{}, I0{});  // j % 6 == 0 here
+  if (j + 1 < nsteps) iteration(j + 1, I1{}, I1{});
+  if (j + 2 < nsteps) iteration(j + 2, I0{}, I2{});
+  if (j + 3 < nsteps) iteration(j + 3, I1{}, I0{});
+  if (j + 4 < nsteps) iteration(j + 4, I0{}, I1{});
 
   // O = acc / l ; lane (c, hf) writes dims dt*32 + 8*g4 + 4*hf + [0, 4) of its query
   const float lt = half_sum(lrun);
