@@ -106,8 +106,18 @@ struct FillCursor {
   int blk;       // LDS byte offset of the slot's block within a stage
 };
 
-template <typename T, int D, int MEMBERS>
-__global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a) {
+// AMODE: 0 plain rows without an anchor prefix; with one member per workgroup
+// also 2, plain rows whose anchor prefix (a_frames whole-chunk anchor frames)
+// every query sees, or 1, per-frame anchor rows (17 fields) where query frame
+// s sees anchor frame s only.  The anchor frames are walked after the HR
+// frames, as extra frame slots with the anchor grid's extent.
+// Two wavefronts per SIMD: the register budget is 256 per lane (the compiler
+// would otherwise reach for accumulation registers and drop to one).
+template <typename T, int D, int MEMBERS, int AMODE>
+__global__ __launch_bounds__(128 * MEMBERS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void window_group_kernel(GroupArgs a) {
+  static_assert(AMODE == 0 || MEMBERS == 1, "anchors run one member per workgroup");
+  constexpr int PST = AMODE == 1 ? 17 : 19;  // params row stride
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr int KS = D / 16;      // k-steps of the S^T MFMA over the head dim
@@ -140,47 +150,73 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   int row0 = gp[0], mt0 = gp[1], row1 = gp[2], mt1 = gp[3];
   row0 = row0 < 0 ? 0 : (row0 >= a.n_w ? a.n_w - 1 : row0);
   row1 = (MEMBERS == 1 || row1 < 0) ? -1 : (row1 >= a.n_w ? a.n_w - 1 : row1);
-  const int32_t* p0 = a.params + static_cast<int64_t>(row0) * 19;
-  const int32_t* p1 = row1 >= 0 ? a.params + static_cast<int64_t>(row1) * 19 : p0;
+  const int32_t* p0 = a.params + static_cast<int64_t>(row0) * PST;
+  const int32_t* p1 = row1 >= 0 ? a.params + static_cast<int64_t>(row1) * PST : p0;
 
   // Shared spatial KV extent (member 0's; the host pairs equal extents) and
   // the two frame ranges.
-  const int kh0 = p0[8], kh_l = p0[9], kw0 = p0[10], kw_l = p0[11];
+  constexpr int F = AMODE == 1 ? -2 : 0;  // field offset of the HR cuboid in a 17-field row
+  const int kh0 = p0[F + 8], kh_l = p0[F + 9], kw0 = p0[F + 10], kw_l = p0[F + 11];
   const int sp = kh_l > 0 && kw_l > 0 ? kh_l * kw_l : 0;
-  const int a0 = p0[6], la = sp > 0 ? max(p0[7], 0) : 0;
-  const int a1 = p1[6], lb = (sp > 0 && row1 >= 0) ? max(p1[7], 0) : 0;
+  const int a0 = p0[F + 6], la = sp > 0 ? max(p0[F + 7], 0) : 0;
+  const int a1 = p1[F + 6], lb = (sp > 0 && row1 >= 0) ? max(p1[F + 7], 0) : 0;
   const int s_lo = max(a0, a1);
   const int nsh = lb > 0 ? max(0, min(a0 + la, a1 + lb) - s_lo) : 0;
   const PrivFrames pf0 = private_frames(a0, la, s_lo, nsh);
   const PrivFrames pf1 = lb > 0 ? private_frames(a1, lb, s_lo, nsh) : PrivFrames{0, 0, 0, 0};
   const PrivFrames pfm = member == 0 ? pf0 : pf1;
   const int P = max(la - nsh, lb > 0 ? lb - nsh : 0);
-  const int nslots = P + nsh;
   const int nS = (sp + GKN - 1) / GKN;
-  const int nsteps = nslots * nS;
   const int first_shared = P * nS;  // steps before it are private (one block per member)
   // This member's frame in slot fs_ (-1: none), without branches.
   auto frame_of = [&](int fs_) __attribute__((always_inline)) -> int {
     const int k2 = fs_ - pfm.len1;
     const int fpriv = fs_ < pfm.len1 ? pfm.lo1 + fs_ : (k2 < pfm.len2 ? pfm.lo2 + k2 : -1);
-    return fs_ < P ? fpriv : (fs_ < nslots ? s_lo + (fs_ - P) : -1);
+    return fs_ < P ? fpriv : (fs_ < P + nsh ? s_lo + (fs_ - P) : -1);
   };
 
   // This wavefront's 32 queries: rows m0 + 32*qhalf + [0, 32) of its member.
   const int my_row = member == 0 ? row0 : row1;
   const int my_mt = member == 0 ? mt0 : mt1;
   const int32_t* pm = member == 0 ? p0 : p1;
-  const int q_t0 = pm[0], q_tl = pm[1], q_h0 = pm[2], q_w0 = pm[3], qh_l = pm[4], qw_l = pm[5];
+  int q_t0, q_tl, q_h0, q_w0, qh_l, qw_l;
+  if constexpr (AMODE == 1) {
+    q_t0 = 0; q_h0 = pm[0]; q_w0 = pm[1]; qh_l = pm[2]; qw_l = pm[3]; q_tl = pm[10];
+  } else {
+    q_t0 = pm[0]; q_tl = pm[1]; q_h0 = pm[2]; q_w0 = pm[3]; qh_l = pm[4]; qw_l = pm[5];
+  }
   const int q_sp = qh_l * qw_l;
   const int lq = q_tl * q_sp;
   const int m0 = 64 * my_mt;
   const bool has_member = my_row >= 0 && qh_l > 0 && qw_l > 0 && q_tl > 0 && m0 >= 0 && m0 < lq;
+
+  // Anchor slots (AMODE 1, 2): n_anc frames of the anchor grid h_a x w_a over
+  // the extent (kh0_a, kh_l_a, kw0_a, kw_l_a), after the HR slots.  AMODE 1
+  // walks the anchor frames f_lo .. f_lo + n_anc - 1 of this tile's query
+  // frames, each admitted to that frame's queries only.
+  int n_anc = 0, kh0_a = 0, kh_l_a = 0, kw0_a = 0, kw_l_a = 0, h_a = 0, w_a = 0, f_lo = 0;
+  if constexpr (AMODE != 0) {
+    const int* pa = pm + (AMODE == 1 ? 11 : 13);
+    kh0_a = pa[0]; kh_l_a = pa[1]; kw0_a = pa[2]; kw_l_a = pa[3]; h_a = pa[4]; w_a = pa[5];
+    const bool anchor_ok = kh_l_a > 0 && kw_l_a > 0 && h_a > 0 && w_a > 0 && has_member;
+    if (AMODE == 1) {
+      f_lo = q_sp > 0 ? m0 / q_sp : 0;
+      const int f_hi = q_sp > 0 ? (min(lq, m0 + 64) - 1) / q_sp : -1;
+      n_anc = anchor_ok ? f_hi - f_lo + 1 : 0;
+    } else {
+      n_anc = anchor_ok ? max(pm[12], 0) : 0;
+    }
+  }
+  const int sp_a = kh_l_a * kw_l_a;
+  const int nS_a = (sp_a + GKN - 1) / GKN;
+  const int nslots = P + nsh + n_anc;
+  const int nsteps = (P + nsh) * nS + n_anc * nS_a;
   // Slots this member consumes a block in, bit fs (the host limits a window
   // to 16 KV frames, so a pair has at most 32 slots).
   uint32_t act = 0;
   if (has_member) {
     for (int fs_ = 0; fs_ < nslots && fs_ < 32; ++fs_)
-      if (frame_of(fs_) >= 0) act |= 1u << fs_;
+      if (fs_ >= P + nsh || frame_of(fs_) >= 0) act |= 1u << fs_;
   }
   auto active = [&](int fs_) __attribute__((always_inline)) -> bool {
     return ((act >> (fs_ & 31)) & 1u) != 0 && fs_ < 32;
@@ -208,10 +244,12 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   const int m = m0 + 32 * qhalf + c;
   const bool qvalid = has_member && m < lq;
   int64_t qflat;
+  int qframe;  // this lane's query frame within the window
   {
     const int mm = qvalid ? m : 0;
     const int qs = q_sp > 0 ? q_sp : 1, qw = qw_l > 0 ? qw_l : 1;
     const int fr = fdiv(mm, qs, 1.0f / static_cast<float>(qs));
+    qframe = fr;
     const int r = mm - fr * q_sp;
     const int hh = fdiv(r, qw, 1.0f / static_cast<float>(qw));
     const int ww = r - hh * qw_l;
@@ -245,32 +283,51 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
   const int s16 = lane & 15;
   const int src_key = (s16 % LPK) * KPI + (lane >> 4) * (16 / LPK) + s16 / LPK;
   const int sub = s16 / LPK;
-  const int kwl = kw_l > 0 ? kw_l : 1;
-  const int dq = GKN / kwl, dr = GKN - dq * kwl;
-  const int row_start = fdiv(src_key, kwl, 1.0f / static_cast<float>(kwl));
-  const int col_start = src_key - row_start * kwl;
-  const int last_tok = (kh_l - 1) * a.W + (kw_l - 1);  // last key of the extent, frame-relative
+  // Walk of a rows x cols extent (row stride rs tokens) 32 keys per step: the
+  // lane's first (row, col), the per-step advance dq rows + dr columns, the
+  // last key of the extent (frame-relative) and the steps per frame.
+  struct Walk {
+    int rows, rs, kwl, dq, dr, row_start, col_start, last_tok, nS;
+  };
+  auto make_walk = [&](int rows, int cols, int rs) __attribute__((always_inline)) -> Walk {
+    Walk g;
+    g.rows = rows; g.rs = rs;
+    g.kwl = cols > 0 ? cols : 1;
+    g.dq = GKN / g.kwl; g.dr = GKN - g.dq * g.kwl;
+    g.row_start = fdiv(src_key, g.kwl, 1.0f / static_cast<float>(g.kwl));
+    g.col_start = src_key - g.row_start * g.kwl;
+    g.last_tok = (rows - 1) * rs + (cols - 1);
+    g.nS = (rows * cols + GKN - 1) / GKN;
+    return g;
+  };
+  const Walk hr_walk = make_walk(kh_l, kw_l, a.W);
   const int frame0_tok = a.hr_base + kh0 * a.W + kw0;
   const KvRing ring = load_ring(a.ring_R, a.ring_nc, a.ring_head);
   auto fbase_of = [&](int fs_) __attribute__((always_inline)) -> int {
+    if (AMODE != 0 && fs_ >= P + nsh) {  // anchor frame: no HR base, no ring
+      const int af = (AMODE == 1 ? f_lo : 0) + (fs_ - P - nsh);
+      return af * h_a * w_a + kh0_a * w_a + kw0_a;
+    }
     const int f = frame_of(fs_);
     return f >= 0 ? frame0_tok + ring_frame(ring, f) * L : -1;
   };
   FillCursor cur;
+  Walk cw = hr_walk;  // the cursor's current extent
   // Per-slot state of the cursor, refreshed when it enters a frame slot.
   auto cursor_slot = [&]() __attribute__((always_inline)) {
     const bool priv = cur.fs < P;
+    if (AMODE != 0 && cur.fs == P + nsh) cw = make_walk(kh_l_a, kw_l_a, w_a);
     cur.fbase = fbase_of(cur.fs);
     cur.part = (priv || member == 0) && cur.fbase >= 0;
     cur.blk = priv ? member * BLKB : 0;
   };
-  cur.fs = 0; cur.s = 0; cur.row = row_start; cur.col = col_start;
+  cur.fs = 0; cur.s = 0; cur.row = cw.row_start; cur.col = cw.col_start;
   cursor_slot();
   constexpr int look = 2;  // steps ahead the fills run
   // Fetch the cursor's step into stage `stage` and advance.
   auto fill_next = [&](int stage) __attribute__((always_inline)) {
     if (__builtin_expect(cur.part, 1)) {  // uniform
-      int t = cur.row < kh_l ? __mul24(cur.row, a.W) + cur.col : last_tok;
+      int t = cur.row < cw.rows ? __mul24(cur.row, cw.rs) + cur.col : cw.last_tok;
       t += cur.fbase;
       t = static_cast<int>(min(static_cast<uint32_t>(t), static_cast<uint32_t>(kv_tokens - 1)));
       const uint32_t dst = lds_fill_base + static_cast<uint32_t>(stage * MEMBERS * BLKB + cur.blk);
@@ -284,17 +341,17 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
         dma_x4(kvrsrc, dst + q * 1024, tq, lo.fill[q]);
       });
     }
-    if (__builtin_expect(++cur.s == nS, 0)) {  // uniform: next frame slot
+    if (__builtin_expect(++cur.s == cw.nS, 0)) {  // uniform: next frame slot
       cur.s = 0;
       ++cur.fs;
-      cur.row = row_start;
-      cur.col = col_start;
       cursor_slot();
+      cur.row = cw.row_start;
+      cur.col = cw.col_start;
     } else {
-      cur.row += dq;
-      cur.col += dr;
-      const bool carry = cur.col >= kwl;
-      cur.col -= carry ? kwl : 0;
+      cur.row += cw.dq;
+      cur.col += cw.dr;
+      const bool carry = cur.col >= cw.kwl;
+      cur.col -= carry ? cw.kwl : 0;
       cur.row += carry ? 1 : 0;
     }
   };
@@ -429,7 +486,9 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
 
   int fs = 0, s = 0;  // frame slot and spatial step of step j
   bool do_pv = nsteps > 0 && active(0);  // the member consumes step j
-  const int tail_valid = sp - (nS - 1) * GKN;  // keys of a frame's last block
+  int nS_c = nS;                               // steps per frame of step j's slot
+  int tail_valid = sp - (nS - 1) * GKN;        // keys of that frame's last block
+  bool admit = true;  // AMODE 1 anchor slots: this lane's query frame is the slot's
   auto iteration = [&](int j, auto stage_c, auto vstage_c) __attribute__((always_inline)) {
     constexpr int stage = decltype(stage_c)::value;    // K stage of step j: j % 2
     constexpr int vstage = decltype(vstage_c)::value;  // V stage of step j: j % VST
@@ -453,10 +512,15 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
     const KOps kf = read_k(std::integral_constant<int, stage ^ 1>{});
     f32x16_t s_next;
     if (__builtin_expect(do_pv, 1)) {  // uniform
-      if (__builtin_expect(s == nS - 1 && tail_valid < GKN, 0)) mask_tail(s_cur, tail_valid);
+      if (__builtin_expect(s == nS_c - 1 && tail_valid < GKN, 0)) mask_tail(s_cur, tail_valid);
+      if (AMODE == 1 && __builtin_expect(fs >= P + nsh, 0)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s_cur[r] = admit ? s_cur[r] : -INFINITY;
+      }
       const VOps vt = read_v(std::integral_constant<int, vstage>{});
       if (__builtin_expect(!minit, 0)) {  // first active block: m = its row max
         mrun = row_max(s_cur);
+        mrun = mrun == -INFINITY ? 0.f : mrun;  // a lane the block does not admit
         shift(s_cur, mrun);
         set_cneg();
         minit = true;
@@ -492,10 +556,15 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
       s_next = s_mfma(kf);
     }
     s_cur = s_next;
-    if (__builtin_expect(++s == nS, 0)) {  // uniform: next frame slot
+    if (__builtin_expect(++s == nS_c, 0)) {  // uniform: next frame slot
       s = 0;
       ++fs;
       do_pv = active(fs);
+      if (AMODE != 0 && fs >= P + nsh && n_anc > 0) {  // anchor slots: the anchor extent
+        nS_c = nS_a;
+        tail_valid = sp_a - (nS_a - 1) * GKN;
+        admit = AMODE != 1 || qframe == f_lo + (fs - P - nsh);
+      }
     }
   };
   // Unrolled by 6 so that both ring stages (j % 2, j % 3) are immediates.
@@ -543,15 +612,19 @@ __global__ __launch_bounds__(128 * MEMBERS) void window_group_kernel(GroupArgs a
 __global__ void clear_amax_kernel(uint32_t* p) { *p = 0u; }
 
 template <typename T, int D>
-int launch_group(const GroupArgs& a, int members, uint32_t grid, hipStream_t stream) {
+int launch_group(const GroupArgs& a, int members, int amode, uint32_t grid, hipStream_t stream) {
   if (a.amax_out) {
     hipLaunchKernelGGL(clear_amax_kernel, dim3(1), dim3(1), 0, stream, a.amax_out);
     SRDIT_LAUNCH_CHECK("clear_amax_kernel");
   }
-  if (members == 1)
-    hipLaunchKernelGGL((window_group_kernel<T, D, 1>), dim3(grid), dim3(128), 0, stream, a);
+  if (amode == 1)
+    hipLaunchKernelGGL((window_group_kernel<T, D, 1, 1>), dim3(grid), dim3(128), 0, stream, a);
+  else if (amode == 2)
+    hipLaunchKernelGGL((window_group_kernel<T, D, 1, 2>), dim3(grid), dim3(128), 0, stream, a);
+  else if (members == 1)
+    hipLaunchKernelGGL((window_group_kernel<T, D, 1, 0>), dim3(grid), dim3(128), 0, stream, a);
   else
-    hipLaunchKernelGGL((window_group_kernel<T, D, 2>), dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((window_group_kernel<T, D, 2, 0>), dim3(grid), dim3(256), 0, stream, a);
   SRDIT_LAUNCH_CHECK("window_group_kernel");
   return SRDIT_OK;
 }
@@ -566,7 +639,7 @@ int group_entry(const char* fn, const void* q, const void* k, const void* v, voi
                 const int32_t* params, const int32_t* groups, int n_w, int n_groups, int hr_base,
                 int H, int W, int64_t q_tokens, int64_t kv_tokens, int n_heads, int head_dim,
                 float scale, int ring_R, int ring_nc, const int32_t* ring_head,
-                uint32_t* amax_out, int members, int dtype, void* stream) {
+                uint32_t* amax_out, int members, int amode, int dtype, void* stream) {
   SRDIT_REQUIRE(q && k && v && o && params && groups, "%s: null pointer", fn);
   SRDIT_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
                 "%s: q/k/v/o must be 16-byte aligned", fn);
@@ -602,11 +675,14 @@ int group_entry(const char* fn, const void* q, const void* k, const void* v, voi
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint32_t grid = static_cast<uint32_t>(grid64);
   SRDIT_REQUIRE(members == 1 || members == 2, "%s: members must be 1 or 2, got %d", fn, members);
+  SRDIT_REQUIRE(amode >= 0 && amode <= 2 && (amode == 0 || members == 1),
+                "%s: anchor mode %d (0 none, 1 per frame, 2 whole chunk) needs one member per "
+                "workgroup", fn, amode);
   if (dtype == SRDIT_DTYPE_BF16)
-    return head_dim == 128 ? launch_group<__bf16, 128>(a, members, grid, s)
-                           : launch_group<__bf16, 64>(a, members, grid, s);
-  return head_dim == 128 ? launch_group<_Float16, 128>(a, members, grid, s)
-                         : launch_group<_Float16, 64>(a, members, grid, s);
+    return head_dim == 128 ? launch_group<__bf16, 128>(a, members, amode, grid, s)
+                           : launch_group<__bf16, 64>(a, members, amode, grid, s);
+  return head_dim == 128 ? launch_group<_Float16, 128>(a, members, amode, grid, s)
+                         : launch_group<_Float16, 64>(a, members, amode, grid, s);
 }
 
 }  // namespace
@@ -619,7 +695,7 @@ extern "C" int srdit_window_attn_grouped_fwd(const void* q, const void* k, const
                                              int head_dim, float scale, int dtype, void* stream) {
   return srdit::group_entry("srdit_window_attn_grouped_fwd", q, k, v, o, params, groups, n_w,
                             n_groups, hr_base, H, W, q_tokens, kv_tokens, n_heads, head_dim,
-                            scale, 0, 0, nullptr, nullptr, 2, dtype, stream);
+                            scale, 0, 0, nullptr, nullptr, 2, 0, dtype, stream);
 }
 
 extern "C" int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, const void* v,
@@ -629,7 +705,8 @@ extern "C" int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, co
                                                 int64_t kv_tokens, int n_heads, int head_dim,
                                                 float scale, int ring_frames, int ring_cached,
                                                 const int32_t* ring_head, uint32_t* amax_out,
-                                                int members, int dtype, void* stream) {
+                                                int members, int anchor_mode, int dtype,
+                                                void* stream) {
   using namespace srdit;
   const char* fn = "srdit_window_attn_grouped_fwd_ex";
   if (ring_frames != 0) {
@@ -644,5 +721,5 @@ extern "C" int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, co
   }
   return group_entry(fn, q, k, v, o, params, groups, n_w, n_groups, hr_base, H, W, q_tokens,
                      kv_tokens, n_heads, head_dim, scale, ring_frames, ring_cached, ring_head,
-                     amax_out, members, dtype, stream);
+                     amax_out, members, anchor_mode, dtype, stream);
 }

@@ -35,7 +35,7 @@ SIGNATURES = {
     "srdit_window_attn_grouped_fwd_ex": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int,
                                                   _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64,
                                                   _c_int, _c_int, _c_f, _c_int, _c_int, _c_p,
-                                                  _c_p, _c_int, _c_int, _c_p]),
+                                                  _c_p, _c_int, _c_int, _c_int, _c_p]),
     "srdit_fp8_quant_rowwise": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p]),
     "srdit_fp8_quant_tensor": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
                                         _c_p]),
@@ -131,19 +131,19 @@ def window_attn_fwd(q, k, v, o, params, order, *, n_w, m_tiles, p_stride, hr_bas
 
 def window_attn_grouped_fwd(q, k, v, o, params, groups, *, n_w, n_groups, hr_base, H, W,
                             n_heads, head_dim, kv_tokens, scale, ring=None, amax_out=None,
-                            members=2):
+                            members=2, anchor_mode=0):
     if q.dtype not in DTYPE_CODES:
         raise ValueError(f"window attention needs bf16 or fp16, got {q.dtype}")
     args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(params), _ptr(groups),
             int(n_w), int(n_groups), int(hr_base), int(H), int(W), int(q.shape[0]),
             int(kv_tokens), int(n_heads), int(head_dim), float(scale))
     tail = (DTYPE_CODES[q.dtype], _stream(q.device))
-    if ring is None and amax_out is None and members == 2:
+    if ring is None and amax_out is None and members == 2 and anchor_mode == 0:
         _check(load().srdit_window_attn_grouped_fwd(*args, *tail),
                "srdit_window_attn_grouped_fwd")
     else:
         _check(load().srdit_window_attn_grouped_fwd_ex(*args, *_ex_args(ring, amax_out),
-                                                       int(members), *tail),
+                                                       int(members), int(anchor_mode), *tail),
                "srdit_window_attn_grouped_fwd_ex")
 
 

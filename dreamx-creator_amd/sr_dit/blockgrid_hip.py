@@ -219,13 +219,43 @@ def build_groups(plan) -> torch.Tensor:
     return torch.tensor(groups, dtype=torch.int32).reshape(-1, 4).contiguous()
 
 
+def _row_lq(plan, row) -> int:
+    """Queries of a params row (plain: q_tl * qh_l * qw_l at fields 1, 4, 5; per-frame
+    anchor rows: fields 10, 2, 3)."""
+    if plan["p_stride"] == P_FRAME:
+        return row[10] * row[2] * row[3]
+    return row[1] * row[4] * row[5]
+
+
+def solo_supported(plan) -> bool:
+    """True when the one-member form of the grouped kernel can run the plan: at
+    most 16 HR KV frames per window and at most 32 frame slots (HR frames plus
+    the anchor frames a 64-query tile walks)."""
+    p = plan["params"]
+    if plan["p_stride"] == P_FRAME:
+        hr = p[:, 5]
+        q_sp = (p[:, 2] * p[:, 3]).clamp(min=1)
+        anc = torch.minimum(p[:, 10], 64 // q_sp + 2)
+    else:
+        hr = p[:, 7]
+        anc = p[:, 12]
+    return bool((hr <= 16).all()) and bool((hr + anc <= 32).all())
+
+
+def plan_anchor_mode(plan) -> int:
+    """Anchor mode code of the grouped kernel: 0 none, 1 per frame, 2 whole chunk."""
+    if plan["p_stride"] == P_FRAME:
+        return 1
+    return 2 if bool((plan["params"][:, 12] > 0).any()) else 0
+
+
 def build_singles(plan) -> torch.Tensor:
     """Every 64-query member alone, in row order: int32 [G, 4] rows (row, m-tile, -1, 0)
     for the one-member-per-workgroup form of the grouped kernel."""
     p = plan["params"].tolist()
     rows = []
     for r, row in enumerate(p):
-        lq = row[1] * row[4] * row[5]
+        lq = _row_lq(plan, row)
         for mt in range(-(-lq // HIP_BLOCK_M) if lq > 0 else 0):
             rows.append((r, mt, -1, 0))
     return torch.tensor(rows, dtype=torch.int32).reshape(-1, 4).contiguous()
@@ -282,12 +312,15 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     ``kernel``: ``"auto"`` runs plain plans without an anchor prefix on the
     grouped kernel: with two members per workgroup sharing their K/V fetches
     (``"grouped"``) when the pairs share nearly all their KV frames (the two
-    m-tiles of one window), else with one member per workgroup (``"solo"``);
-    anchored plans and windows of more than 16 KV frames go to the
-    single-window kernel (``"single"``).  Measured on one MI355X: c2 and c3
-    (neighbouring-frame pairs sharing 2 of 3 frames) and the 48-query shipped
-    windows run fastest solo, c4 (m-tile pairs) grouped.  Any of the three
-    can be forced (a forced grouped or solo launch of an anchored plan raises).
+    m-tiles of one window), else with one member per workgroup (``"solo"``).
+    Anchored plans run solo too (the anchor frames walked after the HR
+    frames); plans beyond its limits (more than 16 HR frames per window, more
+    than 32 frame slots) go to the single-window kernel (``"single"``).
+    Measured on one MI355X: c2 and c3 (neighbouring-frame pairs sharing 2 of
+    3 frames) and the 48-query shipped windows run fastest solo, c4 (m-tile
+    pairs) grouped.  Any of the three can be forced (a forced grouped launch
+    of an anchored plan raises, as does a forced solo launch of a plan beyond
+    its limits).
 
     ``ring`` = ``(ring_frames, ring_cached, head)``: the HR KV after the anchor
     prefix is an in-place cache (``sr_dit.kv_ring.KVRing``): ``ring_frames``
@@ -322,8 +355,13 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     if kernel not in ("auto", "grouped", "solo", "single"):
         raise ValueError("run_blockgrid_hip: kernel must be auto, grouped, solo or single, got "
                          f"{kernel!r}")
-    if kernel in ("grouped", "solo") and not groups_supported(plan):
+    if kernel == "grouped" and not groups_supported(plan):
         raise ValueError("run_blockgrid_hip: the grouped kernel needs plain rows without an anchor.")
+    if kernel == "solo" and not solo_supported(plan):
+        raise ValueError("run_blockgrid_hip: the grouped kernel takes at most 16 HR frames and 32 "
+                         "frame slots per window.")
+    if kernel == "auto" and not groups_supported(plan) and solo_supported(plan):
+        kernel = "solo"
     if kernel == "solo":
         key = ("singles", q.device)
         singles = plan.get(key)
@@ -332,7 +370,8 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
         _lib.window_attn_grouped_fwd(
             q, k_ext, v_ext, out, params, singles, n_w=plan["n_w"], n_groups=singles.shape[0],
             hr_base=hr_base, H=h, W=w, n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0],
-            scale=d ** -0.5, ring=ring, amax_out=amax_out, members=1)
+            scale=d ** -0.5, ring=ring, amax_out=amax_out, members=1,
+            anchor_mode=plan_anchor_mode(plan))
         return out
     use_grouped = False
     if kernel != "single" and groups_supported(plan):

@@ -104,6 +104,11 @@ int srdit_window_attn_grouped_fwd(const void* q, const void* k, const void* v, v
  * members per workgroup of four wavefronts); 1 runs one member per workgroup
  * of two wavefronts (row1 of the groups table is ignored), for tables whose
  * members do not pair.
+ * anchor_mode (grouped only, needs members == 1): 0 plain rows without an
+ * anchor prefix; 2 plain rows with a whole-chunk anchor prefix (a_frames > 0,
+ * the launch srdit_window_attn_fwd mode 0 also runs); 1 per-frame anchor rows
+ * (p_stride 17, as srdit_window_attn_fwd mode 1).  The anchor keys are walked
+ * after the HR keys.
  * Other arguments as srdit_window_attn_fwd / srdit_window_attn_grouped_fwd.
  */
 int srdit_window_attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
@@ -120,7 +125,8 @@ int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, const void* v
                                      int64_t q_tokens, int64_t kv_tokens, int n_heads,
                                      int head_dim, float scale, int ring_frames,
                                      int ring_cached, const int32_t* ring_head,
-                                     uint32_t* amax_out, int members, int dtype, void* stream);
+                                     uint32_t* amax_out, int members, int anchor_mode, int dtype,
+                                     void* stream);
 
 /*
  * Row-wise fp8 e4m3 quantiser: for each row of x [M, K] (row stride ldx),

@@ -33,12 +33,12 @@ def _rand(shape, seed, scale, dtype=torch.bfloat16):
     return (torch.randn(*shape, generator=g) * scale).to(dtype)
 
 
-def _run_spec(spec, anchor_mode, q, k_ext, v_ext):
+def _run_spec(spec, anchor_mode, q, k_ext, v_ext, kernel="auto"):
     plan = bgh.build_plan(spec, anchor_mode=anchor_mode)
     out = torch.empty_like(q)
     n, d = q.shape[1], q.shape[2]
     bgh.run_blockgrid_hip(q, k_ext, v_ext, out, plan=plan, f_cur=spec.f_cur, h=spec.h,
-                          w=spec.w, n=n, d=d, anchor_mode=anchor_mode)
+                          w=spec.w, n=n, d=d, anchor_mode=anchor_mode, kernel=kernel)
     torch.cuda.synchronize()
     return out
 
@@ -93,6 +93,29 @@ def test_small_vs_float64_oracle(name, spec, mode, temp):
     check_attention(out, ref, label=name)
 
 
+ANCHOR_CASES = [c for c in SMALL if c[2] is not None]
+
+
+@pytest.mark.parametrize("name,spec,mode", ANCHOR_CASES, ids=[c[0] for c in ANCHOR_CASES])
+@pytest.mark.parametrize("kernel", ["single", "solo"])
+def test_anchor_plans_both_kernels_vs_float64_oracle(name, spec, mode, kernel):
+    """Anchored plans on the single-window kernel and on the one-member grouped
+    kernel (anchor frames walked after the HR frames), peaky inputs."""
+    n, d = 4, 128
+    g = _geom_of(spec)
+    L = spec.h * spec.w
+    a_h, a_w = g.anchor_grid
+    n_a = spec.f_cur * a_h * a_w
+    sc = d ** -0.5
+    q = _rand((spec.f_cur * L, n, d), 41, sc * 8)
+    k = _rand((n_a + spec.f_kv * L, n, d), 42, sc * 8)
+    v = _rand((n_a + spec.f_kv * L, n, d), 43, sc)
+    print(f"[case] {name} kernel={kernel}", flush=True)
+    out = _run_spec(spec, mode, q.to(DEV), k.to(DEV), v.to(DEV), kernel=kernel)
+    ref = obg.window_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), g, mode)
+    check_attention(out, ref, label=f"{name}/{kernel}")
+
+
 def _gather_ref(spec, mode, q, k_ext, v_ext):
     plan = ogt.GatherPlan(_geom_of(spec), mode, device=q.device)
     return ogt.gather_attend(plan, q.float(), k_ext.float(), v_ext.float(), win_chunk=48)
@@ -115,7 +138,8 @@ def test_benchmark_configs_vs_fp32_gather(cfg, temp):
 
 
 @pytest.mark.parametrize("mode", ["frame", "chunk"])
-def test_production_anchor_geometry(mode):
+@pytest.mark.parametrize("kernel", ["auto", "single"])
+def test_production_anchor_geometry(mode, kernel):
     """Shipped geometry: 4x4 blocks, radius 3, f_cur 3, 12-frame KV, LQ anchor."""
     spec = att._BlockGridSpec(f_cur=3, f_kv=12, h=45, w=80, block_t=3, bh=4, bw=4, rh=3, rw=3,
                               rt=3, streaming=True)
@@ -125,8 +149,8 @@ def test_production_anchor_geometry(mode):
     q = _rand((3 * L, n, d), 21, sc * 4).to(DEV)
     k = _rand((3 * L + 12 * L, n, d), 22, sc * 4).to(DEV)
     v = _rand((3 * L + 12 * L, n, d), 23, sc).to(DEV)
-    print(f"[case] prod anchor={mode}", flush=True)
-    out = _run_spec(spec, mode, q, k, v)
+    print(f"[case] prod anchor={mode} kernel={kernel}", flush=True)
+    out = _run_spec(spec, mode, q, k, v, kernel=kernel)
     ref = _gather_ref(spec, mode, q, k, v)
     check_attention(out, ref, label=f"prod_{mode}")
 
@@ -268,16 +292,25 @@ def test_forced_kernels_on_benchmark_configs(cfg, kernel):
     check_attention(out, _gather_ref(spec, None, q, k, v), label=f"{cfg}/{kernel}")
 
 
-def test_grouped_kernel_refuses_anchor_plans():
+def test_grouped_kernel_limits():
+    """Two members per workgroup: plain rows only; one member: at most 16 HR frames."""
     spec = att._BlockGridSpec(f_cur=2, f_kv=4, h=8, w=12, block_t=2, bh=4, bw=4, rh=1, rw=1,
                               rt=1, streaming=True)
     plan = bgh.build_plan(spec, anchor_mode="chunk")
     q = torch.zeros(2 * 96, 2, 128, dtype=torch.bfloat16, device=DEV)
     kv = torch.zeros(2 * 96 + 4 * 96, 2, 128, dtype=torch.bfloat16, device=DEV)
-    for kernel in ("grouped", "solo"):
-        with pytest.raises(ValueError, match="grouped"):
-            bgh.run_blockgrid_hip(q, kv, kv, torch.empty_like(q), plan=plan, f_cur=2, h=8, w=12,
-                                  n=2, d=128, anchor_mode="chunk", kernel=kernel)
+    with pytest.raises(ValueError, match="grouped"):
+        bgh.run_blockgrid_hip(q, kv, kv, torch.empty_like(q), plan=plan, f_cur=2, h=8, w=12,
+                              n=2, d=128, anchor_mode="chunk", kernel="grouped")
+    long = att._BlockGridSpec(f_cur=3, f_kv=21, h=8, w=12, block_t=3, bh=4, bw=4, rh=1, rw=1,
+                              rt=6, streaming=True)
+    plan = bgh.build_plan(long)
+    assert not bgh.solo_supported(plan)
+    q = torch.zeros(3 * 96, 2, 128, dtype=torch.bfloat16, device=DEV)
+    kv = torch.zeros(21 * 96, 2, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="16 HR frames"):
+        bgh.run_blockgrid_hip(q, kv, kv, torch.empty_like(q), plan=plan, f_cur=3, h=8, w=12,
+                              n=2, d=128, kernel="solo")
 
 
 @pytest.mark.parametrize("cfg,anchor,kernel", [("c3", None, "auto"), ("c2", None, "single"),
