@@ -215,13 +215,15 @@ def refiner_step(model, build_s, steps, warmup):
             "data": "synthetic: N(0,0.02) weights, N(0,1) activations and context"}
 
 
-def stream_chunks(model, chunks=6, timed=2):
+def stream_chunks(model, chunks=6, timed=2, anchor=None):
     """The streaming SR loop at the shipped settings: 45x80-token frames (90x160
     latent), 3-frame chunks, a 9-frame KV cache per layer kept in place (ring),
     4x4-block radius-3 windows, the warped 4-step schedule plus the refresh pass
     per chunk (5 forwards of the 30-layer model), every forward a HIP graph
-    replay.  The first chunks fill the cache (one graph per cache length); the
-    last ``timed`` chunks run at the full 12-frame KV and are timed."""
+    replay.  ``anchor`` "frame": the shipped LQ anchor (run_inference.sh:59-65),
+    harvested per chunk by one more forward over the LQ frames.  The first
+    chunks fill the cache (one graph per cache length); the last ``timed``
+    chunks run at the full 12-frame KV and are timed."""
     import torch
     from sr_dit.stream import StreamingRefiner
 
@@ -231,14 +233,16 @@ def stream_chunks(model, chunks=6, timed=2):
     g = torch.Generator("cpu").manual_seed(0)
     noise = torch.randn(cfg.in_dim, chunk * chunks, 2 * h, 2 * w, generator=g).to(dev)
     ctx = torch.randn(cfg.text_len, cfg.text_dim, generator=g).to(torch.bfloat16).to(dev)
+    lq = torch.randn(cfg.in_dim, chunk * chunks, 2 * h, 2 * w, generator=g).to(dev)
     t0 = time.perf_counter()
-    r = StreamingRefiner(model, h, w, ctx, chunk=chunk, kv_len=9, device=dev)
+    r = StreamingRefiner(model, h, w, ctx, chunk=chunk, kv_len=9, device=dev, anchor=anchor)
     per_chunk = []
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     for c in range(chunks):
+        sl = slice(c * chunk, (c + 1) * chunk)
         e0.record()
-        r.refine_chunk(noise[:, c * chunk:(c + 1) * chunk], c * chunk)
+        r.refine_chunk(noise[:, sl], c * chunk, lq[:, sl] if anchor else None)
         e1.record()
         torch.cuda.synchronize()
         per_chunk.append(e0.elapsed_time(e1))
@@ -248,15 +252,18 @@ def stream_chunks(model, chunks=6, timed=2):
     # one eager forward at the full cache for comparison
     r.use_graph = False
     e0.record()
-    r.forward(noise[:, :chunk], r.steps[0], chunks * chunk)
+    r.forward(noise[:, :chunk], r.steps[0], chunks * chunk, anchored=anchor is not None)
     e1.record()
     torch.cuda.synchronize()
     eager_fwd = e0.elapsed_time(e1)
+    n_fwd = len(r.steps) + 1 + (1 if anchor else 0)
     return {"workload": "streaming SR loop, 5B refiner (30 layers), 3 x 45x80-token chunk vs "
                         "9 cached frames (ring), 4x4 blocks radius 3, 4 denoising steps + "
-                        "KV refresh per chunk, 512 context tokens",
-            "ms_per_chunk": round(ms, 2), "ms_per_forward": round(ms / (len(r.steps) + 1), 2),
-            "eager_ms_per_forward": round(eager_fwd, 2), "forwards_per_chunk": len(r.steps) + 1,
+                        "KV refresh per chunk, 512 context tokens"
+                        + (f", LQ anchor ({anchor}-aligned, harvested per chunk)" if anchor
+                           else ", no LQ anchor"),
+            "ms_per_chunk": round(ms, 2), "ms_per_forward": round(ms / n_fwd, 2),
+            "eager_ms_per_forward": round(eager_fwd, 2), "forwards_per_chunk": n_fwd,
             "steps": [round(t, 2) for t in r.steps], "kv_frames": 9 + chunk,
             "chunk_ms_all": [round(x, 1) for x in per_chunk], "hip_graphs": len(r._graphs),
             "wall_s": round(wall, 1),
@@ -400,6 +407,7 @@ def main():
             result["refiner_step"] = refiner_step(model, build_s, args.step_iters, 1)
         if not args.no_stream:
             result["stream"] = stream_chunks(model)
+            result["stream_lq_anchor"] = stream_chunks(model, anchor="frame")
         del model
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)

@@ -241,7 +241,7 @@ class Block(nn.Module):
                 self.ffn[0], self.ffn[2])
         return all(isinstance(m, Fp8Linear) and m.scaling == "tensor" for m in lins)
 
-    def forward(self, x, e, context, geom, ring=None, cross_kv=None):
+    def forward(self, x, e, context, geom, ring=None, cross_kv=None, kv_out=None):
         """x [s, dim] (bf16), e [1, 6, dim] (fp32), context [lc, dim] -> [s, dim].
 
         ``ring``: this layer's streaming KV cache (``KVRing``, fused path only);
@@ -250,8 +250,9 @@ class Block(nn.Module):
         (models.py:1035-1040) keeps them.
         """
         if FUSED and x.dtype == torch.bfloat16 and self.fusable():
-            return self.forward_fused(x, e, context, geom, ring=ring, cross_kv=cross_kv)
-        if ring is not None or cross_kv is not None:
+            return self.forward_fused(x, e, context, geom, ring=ring, cross_kv=cross_kv,
+                                      kv_out=kv_out)
+        if ring is not None or cross_kv is not None or kv_out is not None:
             raise ValueError("Block: the streaming cache and the cached text K/V need the fused "
                              "forward (bf16 activations, per-tensor Fp8Linear).")
         dt = x.dtype
@@ -266,7 +267,7 @@ class Block(nn.Module):
         return (x.float() + y.float() * ep[5]).to(dt)
 
 
-    def forward_fused(self, x, e, context, geom, ring=None, cross_kv=None):
+    def forward_fused(self, x, e, context, geom, ring=None, cross_kv=None, kv_out=None):
         """The same block with the elementwise chains fused into single-pass kernels.
 
         LayerNorm + modulation (+ the amax of its output), RMSNorm + RoPE and
@@ -280,7 +281,11 @@ class Block(nn.Module):
 
         With a ``ring`` the RMSNorm + RoPE kernel writes K, and the V GEMM
         writes V, straight into the ring's current-chunk region, and the window
-        kernel reads the cached frames in place (no concatenation).
+        kernel reads the cached frames in place (no concatenation); with an
+        anchored geometry (``geom["anchor"]``) it also reads the LQ anchor from
+        the ring's prefix.  ``kv_out = (k, v)`` ([s, dim] views, no ring):
+        where the K and V of this layer go instead of scratch tensors -- the
+        LQ-anchor harvest writes them into the rings' anchor prefixes.
         The window and cross attention write the amax of their outputs, so the
         output projections' quantisers need only their quantise pass.
         """
@@ -306,7 +311,10 @@ class Block(nn.Module):
         _lib.ln_modulate(x, None, None, mod[1], mod[0], self.norm1.eps, attn_in, a0)
         xq, xs = quant_from(attn_in, a0)
         q_lin, k_lin = sa.q.gemm(xq, xs), sa.k.gemm(xq, xs)
-        if ring is None:
+        if ring is None and kv_out is not None:
+            v = sa.v.gemm(xq, xs, out=kv_out[1])
+            k = kv_out[0]
+        elif ring is None:
             v = sa.v.gemm(xq, xs)
             k = torch.empty(s, dim, dtype=bf, device=dev)
         else:
@@ -320,15 +328,20 @@ class Block(nn.Module):
             bgh.run_blockgrid_hip(q.view(s, n, d), k.view(s, n, d), v.view(s, n, d), att_out,
                                   plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d, amax_out=a2)
         elif geom.get("ring_cat"):
-            # the reference's concatenation of the cache with the chunk (tests only)
+            # the reference's concatenation of anchor, cache and chunk (tests only)
             lk, lv = ring.logical(0)
-            bgh.run_blockgrid_hip(q.view(s, n, d), torch.cat([lk, k.view(s, n, d)]),
-                                  torch.cat([lv, v.view(s, n, d)]), att_out, plan=geom["plan"],
-                                  f_cur=f, h=h, w=w, n=n, d=d, amax_out=a2)
+            anc = geom.get("anchor")
+            pk = [ring.anchor_k(0)] if anc else []
+            pv = [ring.anchor_v(0)] if anc else []
+            bgh.run_blockgrid_hip(q.view(s, n, d), torch.cat(pk + [lk, k.view(s, n, d)]),
+                                  torch.cat(pv + [lv, v.view(s, n, d)]), att_out,
+                                  plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d,
+                                  anchor_mode=anc, amax_out=a2)
         else:
             bgh.run_blockgrid_hip(q.view(s, n, d), ring.k[0], ring.v[0], att_out,
                                   plan=geom["plan"], f_cur=f, h=h, w=w, n=n, d=d,
-                                  ring=ring.kernel_ring(), hr_base=ring.A, amax_out=a2)
+                                  anchor_mode=geom.get("anchor"), ring=ring.kernel_ring(),
+                                  hr_base=ring.A, amax_out=a2)
         # the output projection's quantiser reuses the amax the attention wrote
         y = sa.o.gemm(*quant_from(att_out.view(s, dim), a2))
 
@@ -432,24 +445,52 @@ class SRDiT(nn.Module):
         return self._geometry(spec, lc, device, t_offset)
 
     def stream_geometry(self, f, h, w, lc, device, *, cached, chunk=3, t_offset=0,
-                        block_hw=(4, 4), block_radius_hw=(3, 3)):
+                        block_hw=(4, 4), block_radius_hw=(3, 3), anchor=None):
         """Geometry of one streaming chunk: ``f`` query frames against ``cached``
         cached frames plus themselves, under the reference's streaming rule with
         ``block_t = chunk`` and ``rt = f_kv // chunk - 1`` (attention.py:1575-1604
         as models.py:651-676 calls it; the shipped window is 4x4 blocks, radius 3,
-        sr_dit_5b.yaml:45-55)."""
+        sr_dit_5b.yaml:45-55).  ``anchor`` = "frame" / "chunk": the denoising
+        steps' plan with the LQ anchor on the token grid (query frame i sees
+        anchor frame i, or every query frame the whole anchor chunk;
+        attention.py:1520-1565, blockgrid_triton.py:117-133)."""
+        if anchor not in (None, "frame", "chunk"):
+            raise ValueError(f"stream_geometry: anchor must be None, 'frame' or 'chunk', got {anchor!r}.")
         f_kv = int(cached) + f
         spec = att._BlockGridSpec(f_cur=f, f_kv=f_kv, h=h, w=w, block_t=chunk,
                                   bh=block_hw[0], bw=block_hw[1],
                                   rh=block_radius_hw[0], rw=block_radius_hw[1],
                                   rt=max(f_kv // chunk - 1, 0), streaming=True)
+        return self._geometry(spec, lc, device, t_offset, anchor=anchor)
+
+    def harvest_geometry(self, f, h, w, lc, device, *, per_frame=True, chunk=3, t_offset=0,
+                         block_hw=(4, 4), block_radius_hw=(3, 3)):
+        """Geometry of the LQ-anchor harvest forward over ``f`` LQ frames, with no cache
+        (causal_inference.py:426-508).  ``per_frame``: the reference runs each frame
+        as its own one-frame sample at temporal offset ``t_offset + i``; every op but
+        the self-attention is per token, and a one-frame sample's windows see only
+        that frame (rt clamps to 0, attention.py:1598-1603), so this is one forward
+        over the chunk at ``t_offset`` whose windows each see their own frame
+        (``sym_rt = 0``).  Otherwise the whole chunk is one sample without a cache:
+        the non-streaming rule with ``block_t = chunk``."""
+        if per_frame:
+            spec = att._BlockGridSpec(f_cur=f, f_kv=f, h=h, w=w, block_t=chunk,
+                                      bh=block_hw[0], bw=block_hw[1],
+                                      rh=block_radius_hw[0], rw=block_radius_hw[1],
+                                      rt=0, streaming=False, sym_rt=0)
+        else:
+            spec = att._BlockGridSpec(f_cur=f, f_kv=f, h=h, w=w, block_t=chunk,
+                                      bh=block_hw[0], bw=block_hw[1],
+                                      rh=block_radius_hw[0], rw=block_radius_hw[1],
+                                      rt=max(f // chunk - 1, 0), streaming=False)
         return self._geometry(spec, lc, device, t_offset)
 
-    def _geometry(self, spec, lc, device, t_offset):
+    def _geometry(self, spec, lc, device, t_offset, anchor=None):
         cfg = self.cfg
         f, h, w = spec.f_cur, spec.h, spec.w
         rope = rope_table(cfg, f, h, w, t_offset, device)
-        return {"grid": (f, h, w), "plan": bgh.cached_plan(spec),
+        return {"grid": (f, h, w), "plan": bgh.cached_plan(spec, anchor_mode=anchor),
+                "anchor": anchor,
                 "cross": CrossAttentionPlan(f * h * w, lc),
                 "rope": rope,
                 # (cos, sin) pairs [s, head_dim/2] for the fused RMSNorm + RoPE kernel
@@ -471,12 +512,14 @@ class SRDiT(nn.Module):
         e0 = lin(tp[1], F.silu(e)).unflatten(1, (6, self.cfg.dim))
         return e, e0
 
-    def blocks_forward(self, x, e0, context, geom, rings=None, cross=None):
+    def blocks_forward(self, x, e0, context, geom, rings=None, cross=None, kv_outs=None):
         """The 30-block stack: x [s, dim] bf16 -> [s, dim].  ``rings``/``cross``:
-        per-layer streaming KV caches and cached text K/V (or None)."""
+        per-layer streaming KV caches and cached text K/V (or None); ``kv_outs``:
+        per-layer (k, v) destinations of the self-attention K/V (or None)."""
         for i, blk in enumerate(self.blocks):
             x = blk(x, e0, context, geom, ring=None if rings is None else rings[i],
-                    cross_kv=None if cross is None else cross[i])
+                    cross_kv=None if cross is None else cross[i],
+                    kv_out=None if kv_outs is None else kv_outs[i])
         return x
 
     def embed_patches(self, latent):
@@ -507,12 +550,12 @@ class SRDiT(nn.Module):
         and reused by every step (WanT2VCrossAttention.init_cache, models.py:1035-1040)."""
         return [blk.cross_kv(ctx, geom) for blk in self.blocks]
 
-    def forward_embedded(self, latent, e, e0, ctx, geom, rings=None, cross=None):
+    def forward_embedded(self, latent, e, e0, ctx, geom, rings=None, cross=None, kv_outs=None):
         """Patch embedding, blocks and head for an embedded context and timestep:
         latent [in_dim, f, 2h, 2w] -> [out_dim, f, 2h, 2w] fp32."""
         cfg = self.cfg
         x, (f, h, w) = self.embed_patches(latent)
-        x = self.blocks_forward(x, e0, ctx, geom, rings=rings, cross=cross)
+        x = self.blocks_forward(x, e0, ctx, geom, rings=rings, cross=cross, kv_outs=kv_outs)
         return unpatchify(self.head(x, e), (f, h, w), cfg.patch_size, cfg.out_dim)
 
     def forward(self, latent, t, context_raw, geom):

@@ -2,12 +2,13 @@
 KV-cache refresh, on the in-place ring caches and HIP graphs.
 
 Restates the per-chunk loop of CausalInferencePipeline.inference_sr
-(video_refiner/pipeline_sr/causal_inference.py:858-976) for one sample without
-the LQ anchor:
+(video_refiner/pipeline_sr/causal_inference.py:858-976) for one sample:
 
   for each chunk of ``chunk`` latent frames (temporal offset advancing by chunk):
+      [LQ anchor] harvest: model(lq chunk, harvest_t) with no cache; each layer's
+                  K/V of the LQ frames become that layer's anchor (:426-508, :877-899)
       for each timestep t of the step list:
-          flow = model(noisy, t)             # attends the cached frames + the chunk
+          flow = model(noisy, t)             # attends [anchor] + cached frames + the chunk
           x0   = noisy - (t / 1000) * flow   # sr_dit_wrapper.py:551-558, in float64
           if not the last step: noisy = add_noise(x0, randn, next t)
       model(x0, context_noise)               # the refresh pass: its K/V become the cache
@@ -20,10 +21,13 @@ causal_inference.py:278-282 and the sigma_start filter of :831-834.
 
 What is MI355X-specific: the per-layer caches are ``KVRing``s (the refresh
 pass writes the chunk's K/V in place and ``commit`` moves them into the ring,
-no per-call concatenation); the text K/V of every layer are computed once per
-video; and each model forward is one HIP graph replay, captured once per cache
-length (the ring's position is read by the kernels from device memory, so one
-graph serves every chunk once the cache is full).
+no per-call concatenation); the harvest forward writes each layer's anchor K/V
+straight into its ring's anchor prefix, where the window kernels read it (no
+anchor list, no concatenation); the text K/V of every layer are computed once
+per video; and each model forward is one HIP graph replay, captured once per
+kind (harvest, anchored step, plain step) and cache length (the ring's
+position is read by the kernels from device memory, so one graph serves every
+chunk once the cache is full).
 """
 from __future__ import annotations
 
@@ -69,16 +73,37 @@ class StreamingRefiner:
     ``kv_len`` cached frames per layer (sr_dit_5b.yaml:55), ``chunk`` frames per
     step (:45), window ``block_hw``/``block_radius_hw`` (:51-52), step list and
     ``context_noise`` of :10-17.  ``use_graph`` replays each forward from a HIP
-    graph (captured at the first forward with a given cache length).
+    graph (captured at the first forward of each kind and cache length).
     ``ring_cat`` (tests only) makes every layer read the reference's
-    concatenation of its cache with the chunk instead of the ring in place.
+    concatenation of its anchor, cache and chunk instead of the ring in place.
+
+    LQ anchor (run_inference.sh:59-65; causal_inference.py:636-700): ``anchor``
+    "frame" (HR frame i attends LQ frame i; the shipped default) or "chunk"
+    (every HR frame attends the whole LQ chunk), None to run without it.
+    ``anchor_scale`` multiplies the anchor's V (``anchor_mode`` "v") or K
+    ("k") as models.py:638-643 does; a sequence gives one scale per
+    denoising step, as ``lq_guidance_scale`` does (only equal values are
+    supported here).  ``anchor_harvest_t`` is the harvest's timestep (default
+    ``context_noise``, :663-665).
     """
 
     def __init__(self, model, h, w, context_raw, *, chunk=3, kv_len=9,
                  step_list=(1000, 750, 500, 250), warp=True, context_noise=0,
                  sigma_start=1.0, shift=5.0, block_hw=(4, 4), block_radius_hw=(3, 3),
+                 anchor=None, anchor_scale=1.0, anchor_mode="v", anchor_harvest_t=None,
                  use_graph=True, seed=0, device="cuda", ring_cat=False):
         cfg = model.cfg
+        if anchor not in (None, "frame", "chunk"):
+            raise ValueError(f"anchor must be None, 'frame' or 'chunk', got {anchor!r}.")
+        if anchor_mode not in ("k", "v"):
+            raise ValueError(f"anchor_mode must be 'k' or 'v', got {anchor_mode!r}.")
+        scales = ([float(anchor_scale)] if isinstance(anchor_scale, (int, float))
+                  else [float(x) for x in anchor_scale] or [1.0])
+        if any(x != scales[0] for x in scales):
+            raise NotImplementedError("StreamingRefiner: per-step anchor scales must be equal.")
+        self.anchor, self.anchor_mode, self.anchor_scale = anchor, anchor_mode, scales[0]
+        self.harvest_t = float(int(context_noise if anchor_harvest_t is None else anchor_harvest_t))
+        self.sigma_start = float(sigma_start)
         self.model, self.h, self.w, self.chunk = model, h, w, chunk
         self.device = torch.device(device)
         self.block_hw, self.block_radius_hw = tuple(block_hw), tuple(block_radius_hw)
@@ -90,12 +115,13 @@ class StreamingRefiner:
         self.use_graph = use_graph
         self.ring_cat = bool(ring_cat)
         L = h * w
+        a_tok = chunk * L if anchor else 0
         self.rings = [KVRing(1, kv_len, chunk, L, cfg.num_heads, cfg.head_dim,
-                             device=self.device) for _ in model.blocks]
+                             anchor_tokens=a_tok, device=self.device) for _ in model.blocks]
         self.gen = torch.Generator(device=self.device).manual_seed(seed)
         with torch.no_grad():
             self.ctx = model.embed_text(context_raw.to(self.device))
-            g0 = self._geom(0, 0)
+            g0 = self._geom(("plain", 0), 0)
             self.cross = model.cross_cache(self.ctx, g0)
         # static inputs of the captured forwards
         self._lat = torch.zeros(cfg.in_dim, chunk, 2 * h, 2 * w, dtype=torch.float32,
@@ -107,18 +133,24 @@ class StreamingRefiner:
         self.forwards = 0
 
     # ---- one model forward --------------------------------------------------
-    def _geom(self, cached, t_offset):
-        return self.model.stream_geometry(self.chunk, self.h, self.w, self.ctx.shape[0],
-                                          self.device, cached=cached, chunk=self.chunk,
-                                          t_offset=t_offset, block_hw=self.block_hw,
-                                          block_radius_hw=self.block_radius_hw)
+    def _geom(self, key, t_offset):
+        """Geometry of a forward kind: ("harvest", 0), ("anchored", cached) or
+        ("plain", cached)."""
+        kind, cached = key
+        kw = dict(chunk=self.chunk, t_offset=t_offset, block_hw=self.block_hw,
+                  block_radius_hw=self.block_radius_hw)
+        args = (self.chunk, self.h, self.w, self.ctx.shape[0], self.device)
+        if kind == "harvest":
+            return self.model.harvest_geometry(*args, per_frame=self.anchor == "frame", **kw)
+        return self.model.stream_geometry(*args, cached=cached,
+                                          anchor=self.anchor if kind == "anchored" else None, **kw)
 
-    def _static_geom(self, cached, t_offset):
-        """The geometry for this cache length, its RoPE table refreshed in place for
-        ``t_offset`` (so a captured graph sees the new table)."""
-        g = self._geoms.get(cached)
+    def _static_geom(self, key, t_offset):
+        """The geometry for this forward kind and cache length, its RoPE table
+        refreshed in place for ``t_offset`` (so a captured graph sees the new table)."""
+        g = self._geoms.get(key)
         if g is None:
-            g = self._geoms[cached] = self._geom(cached, t_offset)
+            g = self._geoms[key] = self._geom(key, t_offset)
             g["t_offset"] = t_offset
             g["ring_cat"] = self.ring_cat
         elif g["t_offset"] != t_offset:
@@ -132,58 +164,103 @@ class StreamingRefiner:
         return self.model.forward_embedded(self._lat, self._e, self._e0, self.ctx, geom,
                                            rings=self.rings, cross=self.cross)
 
-    def forward(self, latent, t, t_offset):
-        """Flow prediction for the chunk ``latent`` [in_dim, chunk, 2h, 2w] at timestep
-        ``t``, attending the cached frames; writes the chunk's K/V into the rings'
-        current regions (kept only by ``commit``)."""
-        cached = self.rings[0].cached
+    def _run_harvest(self, geom):
+        """The harvest forward: every layer's K/V land in its ring's anchor prefix
+        (the flow output is not used, as causal_inference.py:490-508 keeps only
+        the caches), then the anchor scale (models.py:638-643)."""
+        s, dim = self.chunk * self.h * self.w, self.model.cfg.dim
+        kv = [(r.anchor_k(0).view(s, dim), r.anchor_v(0).view(s, dim)) for r in self.rings]
+        out = self.model.forward_embedded(self._lat, self._e, self._e0, self.ctx, geom,
+                                          cross=self.cross, kv_outs=kv)
+        if self.anchor_scale != 1.0:
+            for r in self.rings:
+                (r.anchor_v(0) if self.anchor_mode == "v" else r.anchor_k(0)).mul_(self.anchor_scale)
+        return out
+
+    def _launch(self, key, t, latent, t_offset, fn):
         with torch.no_grad():
             e, e0 = self.model.time_embed(torch.tensor([float(t)], device=self.device))
             self._e.copy_(e)
             self._e0.copy_(e0)
             self._lat.copy_(latent)
-            geom = self._static_geom(cached, t_offset)
+            geom = self._static_geom(key, t_offset)
             self.forwards += 1
             if not self.use_graph:
-                return self._run(geom)
-            entry = self._graphs.get(cached)
+                return fn(geom)
+            entry = self._graphs.get(key)
             if entry is None:
-                self._run(geom)  # plans, device tables, library handles: outside capture
+                fn(geom)  # plans, device tables, library handles: outside capture
                 torch.cuda.synchronize(self.device)
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph):
-                    out = self._run(geom)
-                entry = self._graphs[cached] = (graph, out)
+                    out = fn(geom)
+                entry = self._graphs[key] = (graph, out)
             entry[0].replay()
             return entry[1]
+
+    def forward(self, latent, t, t_offset, anchored=False):
+        """Flow prediction for the chunk ``latent`` [in_dim, chunk, 2h, 2w] at timestep
+        ``t``, attending the cached frames (and, ``anchored``, the harvested LQ
+        anchor); writes the chunk's K/V into the rings' current regions (kept
+        only by ``commit``)."""
+        kind = "anchored" if anchored and self.anchor is not None else "plain"
+        return self._launch((kind, self.rings[0].cached), t, latent, t_offset, self._run)
+
+    def harvest(self, lq, t_offset):
+        """LQ-anchor harvest of one chunk (causal_inference.py:426-508): ``lq``
+        [in_dim, chunk, 2h, 2w] (the upsampled LR latent), noised to
+        ``anchor_harvest_t`` when that is above 0, through the model at that
+        timestep with no cache; each layer's K/V become its ring's anchor."""
+        if self.anchor is None:
+            raise RuntimeError("StreamingRefiner.harvest: the refiner was built without an anchor.")
+        x = lq
+        if self.harvest_t > 0:
+            sig = self.harvest_t / self.sched.num_train_timesteps
+            noise = torch.randn(lq.shape, generator=self.gen, device=self.device, dtype=lq.dtype)
+            x = (1.0 - sig) * lq + sig * noise
+        self._launch(("harvest", 0), self.harvest_t, x, t_offset, self._run_harvest)
 
     def commit(self):
         for r in self.rings:
             r.commit(self.chunk)
 
     # ---- the loop -----------------------------------------------------------
-    def refine_chunk(self, noisy, t_offset):
+    def refine_chunk(self, noisy, t_offset, lq=None):
         """Denoise one chunk from ``noisy`` (at the first step's noise level) and
-        refresh the caches with it; returns x0 [out_dim, chunk, 2h, 2w] fp32."""
+        refresh the caches with it; returns x0 [out_dim, chunk, 2h, 2w] fp32.
+        ``lq``: the chunk's upsampled LR latent, harvested as the anchor first
+        (required with an anchor)."""
+        if self.anchor is not None:
+            if lq is None:
+                raise ValueError("StreamingRefiner: an anchored refiner needs the LQ chunk.")
+            self.harvest(lq, t_offset)
         x0 = None
         for i, t in enumerate(self.steps):
-            flow = self.forward(noisy, t, t_offset)
+            flow = self.forward(noisy, t, t_offset, anchored=True)
             x0 = (noisy.double() - (t / self.sched.num_train_timesteps) * flow.double()).to(flow.dtype)
             if i + 1 < len(self.steps):
                 noise = torch.randn(x0.shape, generator=self.gen, device=self.device,
                                     dtype=x0.dtype)
                 noisy = self.sched.add_noise(x0, noise, self.steps[i + 1])
-        self.forward(x0, self.context_noise, t_offset)  # refresh pass
+        self.forward(x0, self.context_noise, t_offset)  # refresh pass, no anchor
         self.commit()
         return x0
 
-    def run(self, noise, t_offset=0):
+    def run(self, noise, t_offset=0, lq=None):
         """``noise`` [in_dim, F, 2h, 2w] with F a multiple of ``chunk``: refine every
-        chunk in order; returns the refined latent [out_dim, F, 2h, 2w]."""
+        chunk in order; returns the refined latent [out_dim, F, 2h, 2w].  ``lq``
+        (same shape): the upsampled LR latent; the first noisy input is then
+        ``(1 - sigma_start) * lq + sigma_start * noise`` (causal_inference.py:667-668)
+        and each chunk's anchor is harvested from it."""
         frames = noise.shape[1]
         if frames % self.chunk:
             raise ValueError(f"StreamingRefiner: {frames} frames is not a multiple of {self.chunk}.")
+        if lq is not None and lq.shape != noise.shape:
+            raise ValueError("StreamingRefiner.run: lq and noise must have the same shape.")
+        noisy = noise if lq is None else (1.0 - self.sigma_start) * lq + self.sigma_start * noise
         outs = []
         for c0 in range(0, frames, self.chunk):
-            outs.append(self.refine_chunk(noise[:, c0:c0 + self.chunk], t_offset + c0))
+            sl = slice(c0, c0 + self.chunk)
+            outs.append(self.refine_chunk(noisy[:, sl], t_offset + c0,
+                                          None if lq is None else lq[:, sl]))
         return torch.cat(outs, 1)

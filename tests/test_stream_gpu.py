@@ -7,7 +7,11 @@ wrap), the shipped 4x4/r3 window:
     of its cache with the chunk (causal_inference.py:858-976 through
     attention.py:1506-1510): bit-identical chunks and caches;
   * HIP-graph replays (one graph per cache length, reused while the ring head
-    and the RoPE offset move) against eager forwards.
+    and the RoPE offset move) against eager forwards;
+  * the same with the LQ anchor (both alignments): the harvest forward writes
+    each layer's anchor K/V into its ring's prefix, the denoising steps read
+    it there, against every layer reading the reference's concatenation
+    ``cat([anchor, cache, chunk])`` (attention.py:868-874).
 """
 import pytest
 import torch
@@ -31,10 +35,11 @@ def _inputs(cfg, chunks):
     g = torch.Generator("cpu").manual_seed(5)
     noise = torch.randn(cfg.in_dim, CHUNK * chunks, 2 * H, 2 * W, generator=g).to(DEV)
     ctx = torch.randn(77, cfg.text_dim, generator=g).to(torch.bfloat16).to(DEV)
-    return noise, ctx
+    lq = torch.randn(cfg.in_dim, CHUNK * chunks, 2 * H, 2 * W, generator=g).to(DEV)
+    return noise, ctx, lq
 
 
-def _stream(model, noise, ctx, **kw):
+def _stream(model, noise, ctx, lq=None, **kw):
     r = StreamingRefiner(model, H, W, ctx, chunk=CHUNK, kv_len=KV, seed=1, device=DEV, **kw)
     outs = []
     r.heads_seen = []
@@ -42,13 +47,15 @@ def _stream(model, noise, ctx, **kw):
         r.heads_seen.append(r.rings[0].head)
         print(f"[case] stream chunk {c} cached={r.rings[0].cached} head={r.rings[0].head} {kw}",
               flush=True)
-        outs.append(r.refine_chunk(noise[:, c * CHUNK:(c + 1) * CHUNK], c * CHUNK).clone())
+        sl = slice(c * CHUNK, (c + 1) * CHUNK)
+        outs.append(r.refine_chunk(noise[:, sl], c * CHUNK,
+                                   None if lq is None else lq[:, sl]).clone())
     torch.cuda.synchronize()
     return r, outs
 
 
 def test_stream_ring_in_place_equals_concatenation(refiner_model):
-    noise, ctx = _inputs(refiner_model.cfg, 4)
+    noise, ctx, _ = _inputs(refiner_model.cfg, 4)
     ra, a = _stream(refiner_model, noise, ctx, use_graph=False)
     rb, b = _stream(refiner_model, noise, ctx, use_graph=False, ring_cat=True)
     assert any(hd != 0 for hd in ra.heads_seen)  # a chunk ran with the ring wrapped
@@ -62,13 +69,58 @@ def test_stream_ring_in_place_equals_concatenation(refiner_model):
 
 
 def test_stream_graph_replays_match_eager(refiner_model):
-    noise, ctx = _inputs(refiner_model.cfg, 5)
+    noise, ctx, _ = _inputs(refiner_model.cfg, 5)
     rg, g = _stream(refiner_model, noise, ctx, use_graph=True)
     re_, e = _stream(refiner_model, noise, ctx, use_graph=False)
-    assert sorted(rg._graphs) == [0, 3, 6]  # one graph per cache length
+    assert sorted(rg._graphs) == [("plain", 0), ("plain", 3), ("plain", 6)]  # one per cache length
     for c, (x, y) in enumerate(zip(g, e)):
         err = (x - y).abs().max().item()
         scale = y.abs().max().item()
         print(f"[metrics] chunk {c}: max|graph - eager| = {err:.3e} (max|x0| {scale:.3e})",
+              flush=True)
+        assert err <= 1e-3 * scale, f"chunk {c}"
+
+
+@pytest.mark.parametrize("anchor", ["frame", "chunk"])
+def test_stream_lq_anchor_in_place_equals_concatenation(refiner_model, anchor):
+    noise, ctx, lq = _inputs(refiner_model.cfg, 4)
+    ra, a = _stream(refiner_model, noise, ctx, lq=lq, use_graph=False, anchor=anchor)
+    rb, b = _stream(refiner_model, noise, ctx, lq=lq, use_graph=False, ring_cat=True,
+                    anchor=anchor)
+    assert any(hd != 0 for hd in ra.heads_seen)
+    for c, (x, y) in enumerate(zip(a, b)):
+        assert torch.isfinite(x).all()
+        assert torch.equal(x, y), f"chunk {c}"
+    for la, lb in zip(ra.rings, rb.rings):
+        ka, va = la.logical(0)
+        kb, vb = lb.logical(0)
+        assert torch.equal(ka, kb) and torch.equal(va, vb)
+        assert torch.equal(la.anchor_k(0), lb.anchor_k(0))
+        assert torch.equal(la.anchor_v(0), lb.anchor_v(0))
+        assert torch.isfinite(la.anchor_k(0).float()).all() and la.anchor_v(0).abs().max() > 0
+
+
+def test_stream_lq_anchor_is_used(refiner_model):
+    """The anchored chunk differs from the same chunk without the anchor, and
+    differs again with another LQ input; the refresh pass (no anchor) leaves a
+    cache whose first chunk depends on the anchor only through x0."""
+    noise, ctx, lq = _inputs(refiner_model.cfg, 1)
+    _, a = _stream(refiner_model, noise, ctx, lq=lq, use_graph=False, anchor="frame")
+    _, b = _stream(refiner_model, noise, ctx, use_graph=False)
+    _, c = _stream(refiner_model, noise, ctx, lq=lq.flip(-1), use_graph=False, anchor="frame")
+    assert not torch.equal(a[0], b[0])
+    assert not torch.equal(a[0], c[0])
+
+
+def test_stream_lq_anchor_graph_replays_match_eager(refiner_model):
+    noise, ctx, lq = _inputs(refiner_model.cfg, 4)
+    rg, g = _stream(refiner_model, noise, ctx, lq=lq, use_graph=True, anchor="frame")
+    re_, e = _stream(refiner_model, noise, ctx, lq=lq, use_graph=False, anchor="frame")
+    assert sorted(rg._graphs) == [("anchored", 0), ("anchored", 3), ("anchored", 6),
+                                  ("harvest", 0), ("plain", 0), ("plain", 3), ("plain", 6)]
+    for c, (x, y) in enumerate(zip(g, e)):
+        err = (x - y).abs().max().item()
+        scale = y.abs().max().item()
+        print(f"[metrics] anchored chunk {c}: max|graph - eager| = {err:.3e} (max|x0| {scale:.3e})",
               flush=True)
         assert err <= 1e-3 * scale, f"chunk {c}"

@@ -7,6 +7,7 @@ extra_one_step, as sr_dit_wrapper.py:492-494 builds it), so the warped step
 list of causal_inference.py:280-282 for (1000, 750, 500, 250) is
 1000 * (1, 15/16, 5/6, 5/8).
 """
+import pytest
 import torch
 
 from sr_dit.model import SRDiT, SRDiTConfig
@@ -46,3 +47,69 @@ def test_patch_embedding_gemm_equals_conv3d():
     assert grid == (3, 4, 5)
     ref = ref.flatten(2).transpose(1, 2)[0]
     assert torch.allclose(x, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_per_frame_harvest_plan_is_stacked_one_frame_plans():
+    """The per-frame LQ-anchor harvest runs LR frame i as a one-frame sample with no
+    cache (causal_inference.py:455-500).  The reference's rule for that sample
+    (f_cur = f_kv = 1, block_t = 3, not streaming, rt clamped to 0;
+    attention.py:1583-1603) gives the oracle's one-frame rows; shifted to frame i
+    and stacked, they must equal, row for row, the plan of the single three-frame
+    harvest forward the loop runs instead (``SRDiT.harvest_geometry``)."""
+    import numpy as np
+    from oracle import blockgrid as obg
+
+    cfg = SRDiTConfig(dim=64, ffn_dim=128, num_heads=2, num_layers=0, in_dim=4, out_dim=4,
+                      text_dim=16, text_len=4)
+    m = SRDiT(cfg)
+    for (h, w) in ((45, 80), (16, 24)):
+        geom = m.harvest_geometry(3, h, w, 4, "cpu", per_frame=True, chunk=3,
+                                  block_hw=(4, 4), block_radius_hw=(3, 3))
+        got = geom["plan"]["params"].numpy()
+        one = np.asarray(obg.params_rows(obg.Geometry(
+            f_cur=1, f_kv=1, h=h, w=w, block_t=3, bh=4, bw=4, rh=3, rw=3, rt=0,
+            streaming=False))[0], dtype=np.int64)
+        want = []
+        for t in range(3):
+            r = one.copy()
+            r[:, 0] += t   # q_t0
+            r[:, 6] += t   # kv_t0
+            want.append(r)
+        want = np.concatenate(want)
+        assert got.shape == want.shape
+        assert (got == want).all()
+        # no row lets a frame see another frame
+        assert (got[:, 1] == 1).all() and (got[:, 7] == 1).all() and (got[:, 0] == got[:, 6]).all()
+
+
+def test_whole_chunk_harvest_plan_sees_the_chunk():
+    """per_frame=False: one three-frame sample without a cache; every window sees all
+    three frames (the non-streaming rule with block_t = 3, rt = 0)."""
+    import numpy as np
+    from oracle import blockgrid as obg
+
+    cfg = SRDiTConfig(dim=64, ffn_dim=128, num_heads=2, num_layers=0, in_dim=4, out_dim=4,
+                      text_dim=16, text_len=4)
+    geom = SRDiT(cfg).harvest_geometry(3, 16, 24, 4, "cpu", per_frame=False, chunk=3,
+                                       block_hw=(4, 4), block_radius_hw=(3, 3))
+    got = geom["plan"]["params"].numpy()
+    want = np.asarray(obg.params_rows(obg.Geometry(
+        f_cur=3, f_kv=3, h=16, w=24, block_t=3, bh=4, bw=4, rh=3, rw=3, rt=0,
+        streaming=False))[0], dtype=np.int64)
+    assert (got == want).all()
+    assert (got[:, 6] == 0).all() and (got[:, 7] == 3).all()
+
+
+def test_streaming_refiner_anchor_arguments():
+    from sr_dit.stream import StreamingRefiner
+
+    cfg = SRDiTConfig(dim=64, ffn_dim=128, num_heads=2, num_layers=0, in_dim=4, out_dim=4,
+                      text_dim=16, text_len=4)
+    m = SRDiT(cfg)
+    ctx = torch.zeros(4, 16)
+    with pytest.raises(ValueError):
+        StreamingRefiner(m, 8, 8, ctx, anchor="window", device="cpu")
+    with pytest.raises(ValueError):
+        StreamingRefiner(m, 8, 8, ctx, anchor="frame", anchor_mode="q", device="cpu")
+    with pytest.raises(NotImplementedError):
+        StreamingRefiner(m, 8, 8, ctx, anchor="frame", anchor_scale=[1.0, 0.5], device="cpu")
