@@ -475,6 +475,21 @@ void window_group_kernel(GroupArgs a) {
     for (int dt = 0; dt < DT; ++dt) oacc[dt] = E::mma(vt.t[1][dt], pb, oacc[dt]);
   };
 
+  // Slots this wavefront computes: the member's, less (AMODE 1) the anchor
+  // frames none of its valid queries is admitted to.  Such a slot would add
+  // exp2(-inf) = 0 to every row, so its softmax, P.V and S^T MFMAs are
+  // skipped; the fills go on (both wavefronts share them).
+  uint32_t wact = act;
+  if constexpr (AMODE == 1) {
+    for (int k = 0; k < n_anc; ++k) {
+      const int fs_ = P + nsh + k;
+      if (fs_ < 32 && !__any(qvalid && qframe == f_lo + k)) wact &= ~(1u << fs_);
+    }
+  }
+  auto wactive = [&](int fs_) __attribute__((always_inline)) -> bool {
+    return ((wact >> (fs_ & 31)) & 1u) != 0 && fs_ < 32;
+  };
+
   // Prologue: K and V of steps 0 and 1; S^T of step 0.
   if (nsteps > 0) {
     fill_next(0);
@@ -482,10 +497,10 @@ void window_group_kernel(GroupArgs a) {
   }
   fill_barrier();
   f32x16_t s_cur = f32x16_t{};
-  if (nsteps > 0 && active(0)) s_cur = s_mfma(read_k(std::integral_constant<int, 0>{}));
+  if (nsteps > 0 && wactive(0)) s_cur = s_mfma(read_k(std::integral_constant<int, 0>{}));
 
   int fs = 0, s = 0;  // frame slot and spatial step of step j
-  bool do_pv = nsteps > 0 && active(0);  // the member consumes step j
+  bool do_pv = nsteps > 0 && wactive(0);  // this wavefront consumes step j
   int nS_c = nS;                               // steps per frame of step j's slot
   int tail_valid = sp - (nS - 1) * GKN;        // keys of that frame's last block
   bool admit = true;  // AMODE 1 anchor slots: this lane's query frame is the slot's
@@ -506,9 +521,9 @@ void window_group_kernel(GroupArgs a) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) va[dt] -= BLKB;
     }
-    // The S^T MFMAs run every iteration (on a stale block when the member has
-    // no frame in the next step's slot: that result is never consumed); the
-    // softmax and P.V only for an active step j.
+    // The S^T MFMAs of step j+1 run with the softmax of an active step j (on a
+    // stale block when the wavefront skips step j+1: that result is never
+    // consumed), and otherwise only when step j+1 starts a computed slot.
     const KOps kf = read_k(std::integral_constant<int, stage ^ 1>{});
     f32x16_t s_next;
     if (__builtin_expect(do_pv, 1)) {  // uniform
@@ -552,14 +567,16 @@ void window_group_kernel(GroupArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
       });
-    } else {
+    } else if ((s + 1 == nS_c) && wactive(fs + 1)) {  // uniform: step j+1 starts a computed slot
       s_next = s_mfma(kf);
+    } else {
+      s_next = s_cur;  // step j+1 is skipped too: its scores are never read
     }
     s_cur = s_next;
     if (__builtin_expect(++s == nS_c, 0)) {  // uniform: next frame slot
       s = 0;
       ++fs;
-      do_pv = active(fs);
+      do_pv = wactive(fs);
       if (AMODE != 0 && fs >= P + nsh && n_anc > 0) {  // anchor slots: the anchor extent
         nS_c = nS_a;
         tail_valid = sp_a - (nS_a - 1) * GKN;
