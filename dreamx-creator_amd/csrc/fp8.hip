@@ -1,8 +1,10 @@
 // fp8 e4m3 quantisers and the scaled fp8 GEMM for gfx950.
 //
 // Quantisers (fp8_linear.py:93-103): scale = max(amax * fl32(1/448), 1e-12),
-// q = e4m3(clamp(x / scale, +-448)) with IEEE division and round-to-nearest-even
-// conversion (v_cvt_pk_fp8_f32 writes OCP e4m3fn on gfx950).  The scale is a
+// q = e4m3(clamp(x / scale, +-448)) with the IEEE quotient (formed from the
+// shared scale's reciprocal and one FMA correction, SharedDivisor in
+// fp8_common.h) and round-to-nearest-even conversion (v_cvt_pk_fp8_f32 writes
+// OCP e4m3fn on gfx950).  The scale is a
 // multiply by the fp32 reciprocal because that is what `amax / 448.0` computes
 // on the GPU: torch divides a GPU tensor by a Python scalar as a multiply by
 // the scalar's fp32 reciprocal (and inductor lowers division by a constant the
@@ -99,11 +101,12 @@ __global__ __launch_bounds__(256) void quant_rowwise_kernel(const T* __restrict_
   amax = wave_umax(amax);
   const float s = scale_from_amax_bits(amax);
   if (lane == 0) scale[row] = s;
+  const SharedDivisor sd(s);
   uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
   for (int64_t c = lane; c < nchunk; c += 64) {
     float f[8];
     Load8<T>::get(xr, c, f);
-    qr[c] = to_e4m3x8(f, s);
+    qr[c] = to_e4m3x8(f, sd);
   }
 }
 
@@ -142,6 +145,7 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const T* __restrict__
                                                            const uint32_t* __restrict__ amax_ws) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float s = scale_from_amax_bits(*amax_ws);
+  const SharedDivisor sd(s);
   if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
   const int64_t nchunk = K >> 3;
   for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
@@ -150,7 +154,7 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const T* __restrict__
     for (int64_t c = lane; c < nchunk; c += 64) {
       float f[8];
       Load8<T>::get(xr, c, f);
-      qr[c] = to_e4m3x8(f, s);
+      qr[c] = to_e4m3x8(f, sd);
     }
   }
 }

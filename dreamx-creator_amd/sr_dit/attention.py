@@ -173,7 +173,7 @@ class _BlockGridSpec(NamedTuple):
             ``[max(0, i - rt) * bt, (i + 1) * bt)``; a single run sees the tail
             ``[max(0, f_kv - (rt + 1) * bt), f_kv)``; a sub-block query grid
             sees everything.
-          * ``sym_rt`` set (this build's addition): query frame ``t`` (KV frame
+          * ``sym_rt`` set (an addition, not a reference rule): query frame ``t`` (KV frame
             ``t + f_kv - f_cur``) sees ``[t' - r, t' + r]`` clamped to
             ``[0, f_kv)``.
         """

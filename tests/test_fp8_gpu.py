@@ -308,3 +308,65 @@ def test_quantise_and_gemm_replay_in_a_graph():
         want = m(x)
         torch.cuda.synchronize()
         assert torch.equal(y, want), it
+
+
+def _finite_bf16_values():
+    """Every finite bf16 value (both zeros included), as float32."""
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    finite = ((bits >> 7) & 0xFF) != 0xFF
+    return (bits[finite] << 16).view(np.float32)
+
+
+def _to_bf16_gpu(vals, cols=64):
+    """float32 values that are bf16-exact -> bf16 [rows, cols] on the GPU (zero padded)."""
+    n = len(vals)
+    rows = -(-n // cols)
+    buf = np.zeros(rows * cols, dtype=np.float32)
+    buf[:n] = vals
+    u16 = (buf.view(np.uint32) >> 16).astype(np.uint16)
+    return torch.from_numpy(u16.view(np.int16)).view(torch.bfloat16).reshape(rows, cols).cuda(), buf
+
+
+def test_quant_apply_every_bf16_value_many_scales():
+    """The quantise pass divides by the shared scale through its reciprocal and one
+    FMA correction; over every finite bf16 value |x| <= amax, for amax across the
+    whole float range and at the 1e-12 scale floor, the codes and the scale equal
+    the oracle's (numpy's IEEE x / s, clamp, round-to-nearest-even e4m3)."""
+    vals = _finite_bf16_values()
+    rng = np.random.default_rng(11)
+    amaxes = [448.0, 1.0, 3.0, 0.1, 4.48e-10, 4.4e-10, 1e-30, 1e-40, 3.3895314e38, 2.0 ** -126]
+    amaxes += list((rng.uniform(1.0, 2.0, 48) * 2.0 ** rng.integers(-133, 127, 48)).astype(np.float32))
+    L = _lib()
+    for amax in amaxes:
+        amax32 = np.float32(amax)
+        if not (np.isfinite(amax32) and amax32 > 0):
+            continue
+        x = vals[np.abs(vals) <= amax32]
+        xt, buf = _to_bf16_gpu(x)
+        scale = np.float32(max(np.float32(amax32 * of.INV_FP8_MAX), of.SCALE_FLOOR))
+        want = of.e4m3_encode(np.clip(buf / scale, -of.FP8_MAX, of.FP8_MAX).astype(np.float32))
+        word = torch.from_numpy(np.array([amax32], dtype=np.float32).view(np.int32)).cuda()
+        tq = torch.empty(xt.shape, dtype=F8, device="cuda")
+        ts = torch.empty(1, dtype=torch.float32, device="cuda")
+        L.fp8_quant_apply(xt, tq, ts, word)
+        torch.cuda.synchronize()
+        got = tq.view(torch.uint8).cpu().numpy().reshape(-1)
+        bad = np.nonzero(got != want)[0]
+        assert len(bad) == 0, (f"amax {amax32!r}: {len(bad)} codes differ, first x={buf[bad[0]]!r} "
+                               f"got {got[bad[0]]:#x} want {want[bad[0]]:#x}")
+        assert ts.item() == scale
+
+
+def test_quant_rowwise_every_bf16_value():
+    """All finite bf16 values, sorted by magnitude and cut into rows of 64 (so the row
+    scales span the float range, floor included): codes and scales equal the oracle's."""
+    vals = _finite_bf16_values()
+    vals = vals[np.argsort(np.abs(vals), kind="stable")]
+    xt, buf = _to_bf16_gpu(vals)
+    want_q, want_s = of.quantize_rowwise(buf.reshape(xt.shape))
+    tq = torch.empty(xt.shape, dtype=F8, device="cuda")
+    ts = torch.empty(xt.shape[0], dtype=torch.float32, device="cuda")
+    _lib().fp8_quant_rowwise(xt, tq, ts)
+    torch.cuda.synchronize()
+    assert np.array_equal(ts.cpu().numpy(), want_s)
+    assert np.array_equal(tq.view(torch.uint8).cpu().numpy(), want_q)

@@ -15,7 +15,7 @@ import torch
 from oracle import blockgrid as obg
 from oracle import gather_torch as ogt
 
-from parity import metrics, passes_attention, passes_baseline_tolerance_only
+from parity import metrics, passes_attention, passes_abs_bounds_only
 
 
 def _rand(shape, seed, scale=1.0):
@@ -104,7 +104,7 @@ def test_negative_controls_fail_strengthened_suite():
     uni = np.zeros_like(ref)
     for q_idx, kv_idx in obg.windows(g):
         uni[q_idx] = v[kv_idx].astype(np.float64).mean(0)[None]
-    assert passes_baseline_tolerance_only(uni, ref)
+    assert passes_abs_bounds_only(uni, ref)
     assert not passes_attention(uni, ref), metrics(uni, ref)
     # a mask mistake: every window sees one more frame than it should
     g_bad = obg.Geometry(f_cur=3, f_kv=3, h=24, w=24, block_t=1, bh=8, bw=8, rh=1, rw=1, sym_rt=2)
