@@ -202,47 +202,77 @@ __global__ __launch_bounds__(256) void residual_gate_kernel(const uint16_t* x, i
 
 // RMSNorm over the whole row (K = heads * head_dim), weight w (bf16 [K]), then
 // (ROPE) RoPE on each head: pair j of a head rotated by (cos, sin) = cs[row][j % (head_dim/2)].
-template <bool ROPE>
+// One wavefront per row.  CACHED (K <= 4096): the row stays in registers
+// between the sum of squares and the output pass, its loads all issued first.
+// A chunk of eight values holds pairs 4c .. 4c+3, which (head_dim a multiple
+// of 8) sit at 4c mod (head_dim/2) .. +3 in the table: VEC reads them as two
+// 16-byte loads.  Each lane sums its squares in chunk order either way.
+template <bool ROPE, bool CACHED, bool VEC>
 __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(const uint16_t* __restrict__ x, int64_t M,
                                                            int K, int64_t ldx,
                                                            const uint16_t* __restrict__ w, float eps,
                                                            const float2* __restrict__ cs, int half_d,
                                                            uint16_t* __restrict__ out) {
+  constexpr int CPL = 8;  // cached chunks per lane
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= M) return;
   const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
   const int nc = K >> 3;
-  float ss = 0.f;
-  for (int c = lane; c < nc; c += 64) {
-    float f[8];
-    unpack_bf16x8(xr[c], f);
+  uint4 rb[CACHED ? CPL : 1];
+  if (CACHED) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += __fmul_rn(f[i], f[i]);
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + 64 * i;
+      rb[i] = c < nc ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  auto chunk = [&](int i, int c) -> uint4 { return CACHED ? rb[i] : xr[c]; };
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < (CACHED ? CPL : 1); ++i) {
+    for (int c = lane + 64 * i; c < nc && (CACHED || i == 0); c += (CACHED ? nc : 64)) {
+      float f[8];
+      unpack_bf16x8(chunk(i, c), f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += __fmul_rn(f[e], f[e]);
+    }
   }
   const float r = rsqrtf(__fadd_rn(wave_sum(ss) / static_cast<float>(K), eps));
   const float2* csr = cs + row * half_d;
   uint4* orow = reinterpret_cast<uint4*>(out + row * K);
-  for (int c = lane; c < nc; c += 64) {
-    float f[8], wv[8], o[8];
-    unpack_bf16x8(xr[c], f);
-    unpack_bf16x8(reinterpret_cast<const uint4*>(w)[c], wv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = bf16_round(__fmul_rn(bf16_round(__fmul_rn(f[i], r)), wv[i]));
-    if (ROPE) {
+  for (int i = 0; i < (CACHED ? CPL : 1); ++i) {
+    for (int c = lane + 64 * i; c < nc && (CACHED || i == 0); c += (CACHED ? nc : 64)) {
+      float f[8], wv[8], o[8];
+      unpack_bf16x8(chunk(i, c), f);
+      unpack_bf16x8(reinterpret_cast<const uint4*>(w)[c], wv);
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int j = ((8 * c) >> 1) + p;  // pair index within the row
-        const float2 t = csr[j % half_d];
-        const float a = f[2 * p], bb = f[2 * p + 1];
-        o[2 * p] = __fsub_rn(__fmul_rn(a, t.x), __fmul_rn(bb, t.y));
-        o[2 * p + 1] = __fadd_rn(__fmul_rn(a, t.y), __fmul_rn(bb, t.x));
+      for (int e = 0; e < 8; ++e) f[e] = bf16_round(__fmul_rn(bf16_round(__fmul_rn(f[e], r)), wv[e]));
+      if (ROPE) {
+        const int jb = (4 * c) % half_d;  // first pair of the chunk within its head
+        float2 t[4];
+        if (VEC) {
+          const float4* p4 = reinterpret_cast<const float4*>(csr + jb);
+          const float4 a = p4[0], b = p4[1];
+          t[0] = make_float2(a.x, a.y); t[1] = make_float2(a.z, a.w);
+          t[2] = make_float2(b.x, b.y); t[3] = make_float2(b.z, b.w);
+        } else {
+#pragma unroll
+          for (int p = 0; p < 4; ++p) t[p] = csr[jb + p];
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float a = f[2 * p], bb = f[2 * p + 1];
+          o[2 * p] = __fsub_rn(__fmul_rn(a, t[p].x), __fmul_rn(bb, t[p].y));
+          o[2 * p + 1] = __fadd_rn(__fmul_rn(a, t[p].y), __fmul_rn(bb, t[p].x));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = f[e];
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = f[i];
+      orow[c] = pack_bf16x8(o);
     }
-    orow[c] = pack_bf16x8(o);
   }
 }
 
@@ -338,14 +368,22 @@ extern "C" int srdit_rmsnorm_rope(const void* x, int64_t M, int K, int64_t ldx, 
                 "srdit_rmsnorm_rope: head_dim %d must be a multiple of 8 dividing K=%d", head_dim, K);
   const unsigned blocks = static_cast<unsigned>((M + 3) / 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (rope_cs)
-    rmsnorm_rope_kernel<true><<<blocks, 256, 0, s>>>(
-        static_cast<const uint16_t*>(x), M, K, ldx, static_cast<const uint16_t*>(w), eps,
-        reinterpret_cast<const float2*>(rope_cs), head_dim / 2, static_cast<uint16_t*>(out));
+  const bool cached = K <= 4096, vec = rope_cs != nullptr && aligned16(rope_cs);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* wp = static_cast<const uint16_t*>(w);
+  const float2* cp = reinterpret_cast<const float2*>(rope_cs);
+  uint16_t* op = static_cast<uint16_t*>(out);
+  const int hd = head_dim / 2;
+  if (rope_cs && cached && vec)
+    rmsnorm_rope_kernel<true, true, true><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, eps, cp, hd, op);
+  else if (rope_cs && cached)
+    rmsnorm_rope_kernel<true, true, false><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, eps, cp, hd, op);
+  else if (rope_cs)
+    rmsnorm_rope_kernel<true, false, false><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, eps, cp, hd, op);
+  else if (cached)
+    rmsnorm_rope_kernel<false, true, false><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, eps, nullptr, hd, op);
   else
-    rmsnorm_rope_kernel<false><<<blocks, 256, 0, s>>>(
-        static_cast<const uint16_t*>(x), M, K, ldx, static_cast<const uint16_t*>(w), eps, nullptr,
-        head_dim / 2, static_cast<uint16_t*>(out));
+    rmsnorm_rope_kernel<false, false, false><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, eps, nullptr, hd, op);
   SRDIT_LAUNCH_CHECK("rmsnorm_rope_kernel");
   return SRDIT_OK;
 }
