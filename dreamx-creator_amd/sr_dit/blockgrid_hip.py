@@ -147,6 +147,26 @@ def _window_cost(plan) -> torch.Tensor:
     return lq * lkv
 
 
+def mean_kv_tokens(plan) -> float:
+    """Mean KV tokens per window (HR cuboid plus anchor prefix)."""
+    p = plan["params"].to(torch.int64)
+    if p.shape[0] == 0:
+        return 0.0
+    if plan["p_stride"] == P_FRAME:
+        lkv = p[:, 5] * p[:, 7] * p[:, 9] + p[:, 12] * p[:, 14]
+    else:
+        lkv = p[:, 7] * p[:, 9] * p[:, 11] + p[:, 12] * p[:, 14] * p[:, 16]
+    return float(lkv.double().mean())
+
+
+#: Two members per workgroup pay off only when their shared walk is long: with
+#: fewer KV tokens per window the per-workgroup Q load and O store dominate and
+#: four one-member workgroups per CU hide them better (dense attention over 512
+#: and 1024 context tokens: 193 vs 202 us and 315 vs 318 us; 2048: 556 vs 539 us;
+#: inside the full refiner step the two forms tie).
+GROUPED_MIN_KV = 1536
+
+
 def launch_order(plan) -> torch.Tensor:
     """Window launch order: the planner's own row order (run -> h-block -> w-block).
 
@@ -312,13 +332,15 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     ``kernel``: ``"auto"`` runs plain plans without an anchor prefix on the
     grouped kernel: with two members per workgroup sharing their K/V fetches
     (``"grouped"``) when the pairs share nearly all their KV frames (the two
-    m-tiles of one window), else with one member per workgroup (``"solo"``).
+    m-tiles of one window) and the windows average at least
+    ``GROUPED_MIN_KV`` KV tokens, else with one member per workgroup (``"solo"``).
     Anchored plans run solo too (the anchor frames walked after the HR
     frames); plans beyond its limits (more than 16 HR frames per window, more
     than 32 frame slots) go to the single-window kernel (``"single"``).
     Measured on one MI355X: c2 and c3 (neighbouring-frame pairs sharing 2 of
-    3 frames) and the 48-query shipped windows run fastest solo, c4 (m-tile
-    pairs) grouped.  Any of the three can be forced (a forced grouped launch
+    3 frames), the 48-query shipped windows and dense attention over 512
+    context tokens run fastest solo, c4 (m-tile pairs, 2733 KV tokens on
+    average) grouped.  Any of the three can be forced (a forced grouped launch
     of an anchored plan raises, as does a forced solo launch of a plan beyond
     its limits).
 
@@ -381,11 +403,13 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
             host = build_groups(plan)
             plan["groups_paired_fraction"] = paired_fraction(host)
             plan["groups_shared_fraction"] = shared_fraction(plan, host)
+            plan["mean_kv_tokens"] = mean_kv_tokens(plan)
             groups = plan[key] = host.to(q.device)
         # Pairs that share only part of their KV frames, and unpaired members,
         # run faster one member per workgroup.
         use_grouped = kernel == "grouped" or (plan["groups_paired_fraction"] >= 0.75 and
-                                              plan["groups_shared_fraction"] >= 0.9)
+                                              plan["groups_shared_fraction"] >= 0.9 and
+                                              plan["mean_kv_tokens"] >= GROUPED_MIN_KV)
         if not use_grouped:
             return run_blockgrid_hip(q, k_ext, v_ext, out, plan=plan, f_cur=f_cur, h=h, w=w, n=n,
                                      d=d, anchor_mode=anchor_mode, kernel="solo", ring=ring,

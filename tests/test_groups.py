@@ -114,3 +114,15 @@ def test_shared_fraction_separates_mtile_pairs_from_frame_pairs():
     assert bgh.shared_fraction(c4, bgh.build_groups(c4)) == 1.0
     assert bgh.shared_fraction(c3, bgh.build_groups(c3)) == 0.75
     assert bgh.shared_fraction(c3, bgh.build_singles(c3)) == 0.0
+
+
+def test_grouped_form_needs_long_shared_walks():
+    """Two members per workgroup only where pairs share their KV and the walk is long:
+    c4's m-tile pairs (2733 KV tokens per window on average) qualify, dense attention
+    over 512 context tokens (every pair shares everything) does not."""
+    from sr_dit.model import CrossAttentionPlan
+    c4 = bgh.build_plan(wl.window_spec("c4"))
+    assert bgh.mean_kv_tokens(c4) >= bgh.GROUPED_MIN_KV
+    cross = CrossAttentionPlan(21600, 512).plan
+    assert bgh.mean_kv_tokens(cross) == 512.0 < bgh.GROUPED_MIN_KV
+    assert bgh.shared_fraction(cross, bgh.build_groups(cross)) == 1.0
