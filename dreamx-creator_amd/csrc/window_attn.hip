@@ -322,8 +322,12 @@ __global__ __launch_bounds__(64 * WAVES) void window_attn_kernel(WinArgs a) {
             (q_w0 + ww);
     qflat = qflat < 0 ? 0 : (qflat >= a.q_tokens ? a.q_tokens - 1 : qflat);
     const V8* qp = reinterpret_cast<const V8*>(qb + qflat * tok + hf * (D / 2));
+    // Every lane loads (qflat is clamped in bounds): no exec branch between
+    // the loads; lanes past the window's queries are zeroed after the load.
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) st.qf[ks] = qvalid ? qp[ks] : V8{};
+    for (int ks = 0; ks < KS; ++ks) st.qf[ks] = qp[ks];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) st.qf[ks] = qvalid ? st.qf[ks] : V8{};
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) st.oacc[dt] = f32x16_t{};
     st.mrun = -INFINITY;

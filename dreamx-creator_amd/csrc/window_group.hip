@@ -260,12 +260,17 @@ void window_group_kernel(GroupArgs a) {
                                                qflat * tok + hf * (D / 2));
     // Q enters the S^T MFMA pre-scaled by scale*log2(e) (rounded once to T),
     // so the scores come out in log2 units.
+    // Every lane loads (qflat is clamped in bounds), so the loads issue back to
+    // back with no exec branches between them; lanes past the window's queries
+    // are zeroed after the load.
+    V8 raw[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) raw[ks] = qp[ks];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const V8 raw = qvalid ? qp[ks] : V8{};
       float x[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(raw[i]) * a.scale_log2;
+      for (int i = 0; i < 8; ++i) x[i] = qvalid ? static_cast<float>(raw[ks][i]) * a.scale_log2 : 0.f;
       qf[ks] = E::pack8(x);
     }
 #pragma unroll
