@@ -2,6 +2,7 @@
 import itertools
 
 import pytest
+import torch
 
 from sr_dit import blockgrid_hip as bgh
 from sr_dit import workloads as wl
@@ -126,3 +127,28 @@ def test_grouped_form_needs_long_shared_walks():
     cross = CrossAttentionPlan(21600, 512).plan
     assert bgh.mean_kv_tokens(cross) == 512.0 < bgh.GROUPED_MIN_KV
     assert bgh.shared_fraction(cross, bgh.build_groups(cross)) == 1.0
+
+
+@pytest.mark.parametrize("cfg", ["c2", "c3", "c4", "prod", "prod_frame"])
+def test_singles_order_heaviest_first_within_runs(cfg):
+    """One-member launch table: every (row, m-tile) exactly once, query runs in plan
+    order, and within a run the windows by non-increasing cost."""
+    from sr_dit import attention as att
+    if cfg.startswith("prod"):
+        spec = att._BlockGridSpec(f_cur=3, f_kv=12, h=45, w=80, block_t=3, bh=4, bw=4, rh=3, rw=3,
+                                  rt=3, streaming=True)
+        plan = bgh.build_plan(spec, anchor_mode="frame" if cfg == "prod_frame" else None)
+    else:
+        plan = bgh.build_plan(wl.window_spec(cfg))
+    s = bgh.build_singles(plan)
+    p = plan["params"]
+    want = {(r, mt) for r in range(p.shape[0])
+            for mt in range(-(-bgh._row_lq(plan, p[r].tolist()) // bgh.HIP_BLOCK_M))}
+    got = [tuple(x) for x in s[:, :2].tolist()]
+    assert len(got) == len(want) and set(got) == want
+    assert (s[:, 2] == -1).all()
+    cost = bgh._window_cost(plan)[s[:, 0].long()]
+    run = p[s[:, 0].long(), 0] if plan["p_stride"] == bgh.P_PLAIN else torch.zeros(len(s))
+    assert (run[1:] >= run[:-1]).all()
+    same = run[1:] == run[:-1]
+    assert (cost[1:][same] <= cost[:-1][same]).all()
