@@ -204,8 +204,10 @@ def build_groups(plan) -> torch.Tensor:
     same spatial KV extent (kh0, khL, kw0, kwL) and an overlapping frame range
     (the neighbouring query frames of the +-1-frame and streaming rules); those
     pairs share the K/V fetches of their common frames.  Unpaired members run
-    alone (row1 = -1).  Groups are ordered by their first member's row, the
-    planner's raster order.
+    alone (row1 = -1).  Groups are ordered by the query run of their first
+    member, then heaviest first (both members' Lq * Lkv; stable, so equal
+    groups keep the planner's raster order), as ``build_singles`` orders its
+    members: c4's m-tile pairs 280.5 -> 272.7 us.
     """
     p = plan["params"].tolist()
     singles = []
@@ -236,7 +238,10 @@ def build_groups(plan) -> torch.Tensor:
             groups.append((r0, m0, -1, 0))
             i += 1
     groups.sort(key=lambda g: (g[0], g[1]))
-    return torch.tensor(groups, dtype=torch.int32).reshape(-1, 4).contiguous()
+    cost = _window_cost(plan).tolist()
+    weight = [cost[g[0]] + (cost[g[2]] if g[2] >= 0 else 0) for g in groups]
+    order = sorted(range(len(groups)), key=lambda i: (p[groups[i][0]][0], -weight[i]))
+    return torch.tensor([groups[i] for i in order], dtype=torch.int32).reshape(-1, 4).contiguous()
 
 
 def _row_lq(plan, row) -> int:

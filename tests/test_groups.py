@@ -152,3 +152,16 @@ def test_singles_order_heaviest_first_within_runs(cfg):
     assert (run[1:] >= run[:-1]).all()
     same = run[1:] == run[:-1]
     assert (cost[1:][same] <= cost[:-1][same]).all()
+
+
+@pytest.mark.parametrize("cfg", ["c2", "c3", "c4"])
+def test_groups_order_heaviest_first_within_runs(cfg):
+    plan = bgh.build_plan(wl.window_spec(cfg))
+    g = bgh.build_groups(plan)
+    p = plan["params"]
+    cost = bgh._window_cost(plan)
+    w = cost[g[:, 0].long()] + torch.where(g[:, 2] >= 0, cost[g[:, 2].clamp(min=0).long()], 0)
+    run = p[g[:, 0].long(), 0]
+    assert (run[1:] >= run[:-1]).all()
+    same = run[1:] == run[:-1]
+    assert (w[1:][same] <= w[:-1][same]).all()
