@@ -124,3 +124,33 @@ def test_stream_lq_anchor_graph_replays_match_eager(refiner_model):
         print(f"[metrics] anchored chunk {c}: max|graph - eager| = {err:.3e} (max|x0| {scale:.3e})",
               flush=True)
         assert err <= 1e-3 * scale, f"chunk {c}"
+
+
+def test_stream_anchor_scale_mode_and_harvest_noise(refiner_model):
+    """The anchor scale multiplies V (mode "v") or K (mode "k") of the harvested
+    anchor, rounded to bf16 as models.py:638-643 computes it (a scale of 0.5 is
+    exact); a harvest at timestep > 0 noises the LQ input first
+    (causal_inference.py:468-471) and gives another, finite anchor."""
+    _, ctx, lq = _inputs(refiner_model.cfg, 1)
+    chunk = lq[:, :CHUNK]
+
+    def harvested(**kw):
+        r = StreamingRefiner(refiner_model, H, W, ctx, chunk=CHUNK, kv_len=KV, seed=1, device=DEV,
+                             use_graph=False, anchor="frame", **kw)
+        print(f"[case] harvest {kw}", flush=True)
+        r.harvest(chunk, 0)
+        torch.cuda.synchronize()
+        return [(ring.anchor_k(0).clone(), ring.anchor_v(0).clone()) for ring in r.rings]
+
+    base = harvested()
+    for mode in ("v", "k"):
+        scaled = harvested(anchor_scale=0.5, anchor_mode=mode)
+        for (k0, v0), (k1, v1) in zip(base, scaled):
+            if mode == "v":
+                assert torch.equal(k1, k0) and torch.equal(v1, (v0.float() * 0.5).to(v0.dtype))
+            else:
+                assert torch.equal(v1, v0) and torch.equal(k1, (k0.float() * 0.5).to(k0.dtype))
+    noised = harvested(anchor_harvest_t=500)
+    for (k0, v0), (k1, v1) in zip(base, noised):
+        assert torch.isfinite(k1.float()).all() and torch.isfinite(v1.float()).all()
+        assert not torch.equal(v1, v0)
