@@ -82,9 +82,9 @@ class StreamingRefiner:
     (every HR frame attends the whole LQ chunk), None to run without it.
     ``anchor_scale`` multiplies the anchor's V (``anchor_mode`` "v") or K
     ("k") as models.py:638-643 does; a sequence gives one scale per
-    denoising step, as ``lq_guidance_scale`` does (only equal values are
-    supported here).  ``anchor_harvest_t`` is the harvest's timestep (default
-    ``context_noise``, :663-665).
+    denoising step, the last one repeating, as ``lq_guidance_scale`` does
+    (causal_inference.py:904-906).  ``anchor_harvest_t`` is the harvest's
+    timestep (default ``context_noise``, :663-665).
     """
 
     def __init__(self, model, h, w, context_raw, *, chunk=3, kv_len=9,
@@ -99,9 +99,11 @@ class StreamingRefiner:
             raise ValueError(f"anchor_mode must be 'k' or 'v', got {anchor_mode!r}.")
         scales = ([float(anchor_scale)] if isinstance(anchor_scale, (int, float))
                   else [float(x) for x in anchor_scale] or [1.0])
-        if any(x != scales[0] for x in scales):
-            raise NotImplementedError("StreamingRefiner: per-step anchor scales must be equal.")
-        self.anchor, self.anchor_mode, self.anchor_scale = anchor, anchor_mode, scales[0]
+        self.anchor, self.anchor_mode, self.anchor_scales = anchor, anchor_mode, scales
+        # One scale: applied once, in the harvest.  Several: the harvest keeps the
+        # unscaled anchor aside and each anchored step writes its scaled copy.
+        self._vary_scale = anchor is not None and any(x != scales[0] for x in scales)
+        self.anchor_scale = 1.0 if self._vary_scale else scales[0]
         self.harvest_t = float(int(context_noise if anchor_harvest_t is None else anchor_harvest_t))
         self.sigma_start = float(sigma_start)
         self.model, self.h, self.w, self.chunk = model, h, w, chunk
@@ -131,6 +133,10 @@ class StreamingRefiner:
         self._geoms = {}
         self._graphs = {}
         self.forwards = 0
+        self._anchor_src = None
+        if self._vary_scale:
+            self._anchor_src = [torch.empty_like(self._scaled_part(r)) for r in self.rings]
+            self._scale_dev = torch.ones(1, dtype=torch.float32, device=self.device)
 
     # ---- one model forward --------------------------------------------------
     def _geom(self, key, t_offset):
@@ -164,6 +170,18 @@ class StreamingRefiner:
         return self.model.forward_embedded(self._lat, self._e, self._e0, self.ctx, geom,
                                            rings=self.rings, cross=self.cross)
 
+    def _scaled_part(self, ring):
+        return ring.anchor_v(0) if self.anchor_mode == "v" else ring.anchor_k(0)
+
+    def _run_anchored(self, geom):
+        """An anchored step; with per-step scales the anchor is first rewritten as
+        bf16(unscaled * scale), the scale read from device memory (so one captured
+        graph serves every step)."""
+        if self._vary_scale:
+            for r, src in zip(self.rings, self._anchor_src):
+                torch.mul(src, self._scale_dev, out=self._scaled_part(r))
+        return self._run(geom)
+
     def _run_harvest(self, geom):
         """The harvest forward: every layer's K/V land in its ring's anchor prefix
         (the flow output is not used, as causal_inference.py:490-508 keeps only
@@ -172,9 +190,12 @@ class StreamingRefiner:
         kv = [(r.anchor_k(0).view(s, dim), r.anchor_v(0).view(s, dim)) for r in self.rings]
         out = self.model.forward_embedded(self._lat, self._e, self._e0, self.ctx, geom,
                                           cross=self.cross, kv_outs=kv)
-        if self.anchor_scale != 1.0:
+        if self._vary_scale:
+            for r, src in zip(self.rings, self._anchor_src):
+                src.copy_(self._scaled_part(r))
+        elif self.anchor_scale != 1.0:
             for r in self.rings:
-                (r.anchor_v(0) if self.anchor_mode == "v" else r.anchor_k(0)).mul_(self.anchor_scale)
+                self._scaled_part(r).mul_(self.anchor_scale)
         return out
 
     def _launch(self, key, t, latent, t_offset, fn):
@@ -204,7 +225,8 @@ class StreamingRefiner:
         anchor); writes the chunk's K/V into the rings' current regions (kept
         only by ``commit``)."""
         kind = "anchored" if anchored and self.anchor is not None else "plain"
-        return self._launch((kind, self.rings[0].cached), t, latent, t_offset, self._run)
+        fn = self._run_anchored if kind == "anchored" else self._run
+        return self._launch((kind, self.rings[0].cached), t, latent, t_offset, fn)
 
     def harvest(self, lq, t_offset):
         """LQ-anchor harvest of one chunk (causal_inference.py:426-508): ``lq``
@@ -236,6 +258,8 @@ class StreamingRefiner:
             self.harvest(lq, t_offset)
         x0 = None
         for i, t in enumerate(self.steps):
+            if self._vary_scale:
+                self._scale_dev.fill_(self.anchor_scales[min(i, len(self.anchor_scales) - 1)])
             flow = self.forward(noisy, t, t_offset, anchored=True)
             x0 = (noisy.double() - (t / self.sched.num_train_timesteps) * flow.double()).to(flow.dtype)
             if i + 1 < len(self.steps):

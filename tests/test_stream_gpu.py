@@ -154,3 +154,26 @@ def test_stream_anchor_scale_mode_and_harvest_noise(refiner_model):
     for (k0, v0), (k1, v1) in zip(base, noised):
         assert torch.isfinite(k1.float()).all() and torch.isfinite(v1.float()).all()
         assert not torch.equal(v1, v0)
+
+
+def test_stream_per_step_anchor_scales(refiner_model):
+    """Per-step anchor scales (lq_guidance_scale as a list, causal_inference.py:904-906):
+    step i reads bf16(unscaled anchor * scale_i), the last scale repeating; the kept
+    unscaled anchor is the one-scale harvest; graph replays (the scale read from device
+    memory) equal eager forwards; and the scales change the result."""
+    noise, ctx, lq = _inputs(refiner_model.cfg, 2)
+    scales = [1.0, 0.5, 2.0]  # four steps: the last two use 2.0
+    rg, g = _stream(refiner_model, noise, ctx, lq=lq, use_graph=True, anchor="frame",
+                    anchor_scale=scales)
+    re_, e = _stream(refiner_model, noise, ctx, lq=lq, use_graph=False, anchor="frame",
+                     anchor_scale=scales)
+    r1, one = _stream(refiner_model, noise, ctx, lq=lq, use_graph=False, anchor="frame")
+    for c, (x, y) in enumerate(zip(g, e)):
+        err = (x - y).abs().max().item()
+        print(f"[metrics] per-step scales chunk {c}: max|graph - eager| = {err:.3e}", flush=True)
+        assert err <= 1e-3 * y.abs().max().item(), f"chunk {c}"
+    for ring_e, src, ring_1 in zip(re_.rings, re_._anchor_src, r1.rings):
+        assert torch.equal(src, ring_1.anchor_v(0))
+        assert torch.equal(ring_e.anchor_v(0), (src.float() * 2.0).to(src.dtype))
+        assert torch.equal(ring_e.anchor_k(0), ring_1.anchor_k(0))
+    assert not torch.equal(e[0], one[0])

@@ -111,5 +111,3 @@ def test_streaming_refiner_anchor_arguments():
         StreamingRefiner(m, 8, 8, ctx, anchor="window", device="cpu")
     with pytest.raises(ValueError):
         StreamingRefiner(m, 8, 8, ctx, anchor="frame", anchor_mode="q", device="cpu")
-    with pytest.raises(NotImplementedError):
-        StreamingRefiner(m, 8, 8, ctx, anchor="frame", anchor_scale=[1.0, 0.5], device="cpu")
