@@ -342,3 +342,62 @@ def test_output_amax_word(cfg, anchor, kernel):
     assert torch.equal(out, ref)
     want = out.float().abs().max().view(torch.int32)
     assert int(word) == int(want)
+
+
+PAR_CASES = {
+    # name: (f_cur, extra op kwargs, expected spec fields as the reference derives them,
+    #        attention.py:1583-1604: no cache and no anchor -> not streaming)
+    "chunk_causal": (9, dict(causal_chunk_frames=3, causal_kv_span=6),
+                     dict(hist=None, rt=1, chunk_frames=3)),          # rt = span // bt - 1
+    "radius_t": (9, dict(causal_chunk_frames=3, block_radius_t=1),
+                 dict(hist=9, rt=2, chunk_frames=3)),                 # hist = (2 r_t + 1) bt
+    "legacy_rt": (9, dict(), dict(hist=None, rt=2, chunk_frames=None)),  # rt = f_kv // bt - 1
+}
+
+
+@pytest.mark.parametrize("case", sorted(PAR_CASES))
+def test_op_entry_parallel_forward_rules(case):
+    """The op's own derivation of the temporal rule for a forward without a cache:
+    the chunk-causal span of the parallel forward (models.py:647-650), the
+    chunk-anchored history of block_radius_t, and the legacy rt rule; the output
+    matches the oracle on the spec the reference derives."""
+    f, h, w, n, d = PAR_CASES[case][0], 16, 24, 4, 128
+    L = h * w
+    sc = d ** -0.5
+    q = _rand((1, f * L, n, d), 61, sc * 4).to(DEV)
+    k = _rand((1, f * L, n, d), 62, sc * 4).to(DEV)
+    v = _rand((1, f * L, n, d), 63, sc).to(DEV)
+    grid = torch.tensor([[f, h, w]])
+    print(f"[case] op parallel rule {case}", flush=True)
+    out, _, _ = att.mask_free_window_attention(q, k, v, grid, attn_impl="hip", block_t=3,
+                                               block_hw=(4, 4), block_radius_hw=(2, 2),
+                                               **PAR_CASES[case][1])
+    torch.cuda.synchronize()
+    spec = att._BlockGridSpec(f_cur=f, f_kv=f, h=h, w=w, block_t=3, bh=4, bw=4, rh=2, rw=2,
+                              streaming=False, **PAR_CASES[case][2])
+    ref = _gather_ref(spec, None, q[0], k[0], v[0])
+    check_attention(out[0], ref, label=f"op {case}")
+
+
+def test_op_entry_anchor_keep():
+    """anchor_keep False drops a sample's anchor (attention.py:1560-1565): the output
+    equals the call without an anchor; True keeps it and changes the output."""
+    h, w, n, d = 16, 24, 4, 128
+    L = h * w
+    sc = d ** -0.5
+    q = _rand((1, 3 * L, n, d), 71, sc * 4).to(DEV)
+    k = _rand((1, 3 * L, n, d), 72, sc * 4).to(DEV)
+    v = _rand((1, 3 * L, n, d), 73, sc).to(DEV)
+    ak = _rand((1, 3 * L, n, d), 74, sc * 4).to(DEV)
+    av = _rand((1, 3 * L, n, d), 75, sc).to(DEV)
+    grid = torch.tensor([[3, h, w]])
+    kw = dict(attn_impl="hip", block_t=3, block_hw=(4, 4), block_radius_hw=(2, 2))
+    print("[case] op anchor_keep", flush=True)
+    plain, _, _ = att.mask_free_window_attention(q, k, v, grid, **kw)
+    dropped, _, _ = att.mask_free_window_attention(q, k, v, grid, anchor_k=ak, anchor_v=av,
+                                                   anchor_keep=[False], **kw)
+    kept, _, _ = att.mask_free_window_attention(q, k, v, grid, anchor_k=ak, anchor_v=av,
+                                                anchor_keep=[True], **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(dropped, plain)
+    assert not torch.equal(kept, plain)
