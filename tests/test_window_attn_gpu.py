@@ -218,18 +218,40 @@ def test_deterministic():
     assert torch.equal(a, b)
 
 
-def test_fp16_and_head_dim_64():
+@pytest.mark.parametrize("kernel", ["single", "solo", "grouped"])
+def test_fp16_and_head_dim_64(kernel):
     spec = att._BlockGridSpec(f_cur=3, f_kv=3, h=16, w=16, block_t=1, bh=8, bw=8, rh=1, rw=1,
                               sym_rt=1)
     g = _geom_of(spec)
     for dtype, d in ((torch.float16, 128), (torch.bfloat16, 64), (torch.float16, 64)):
+        print(f"[case] {kernel} {dtype} d={d}", flush=True)
         q = _rand((3 * 256, 3, d), 41, d ** -0.5 * 4, dtype)
         k = _rand((3 * 256, 3, d), 42, d ** -0.5 * 4, dtype)
         v = _rand((3 * 256, 3, d), 43, 1.0, dtype)
-        out = _run_spec(spec, None, q.to(DEV), k.to(DEV), v.to(DEV))
+        out = _run_spec(spec, None, q.to(DEV), k.to(DEV), v.to(DEV), kernel=kernel)
         ref = obg.window_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), g)
         rel = metrics(out, ref)["rel_l2"]
         assert rel < 4e-3, (dtype, d, rel)
+
+
+@pytest.mark.parametrize("mode", ["frame", "chunk"])
+@pytest.mark.parametrize("kernel", ["single", "solo"])
+def test_anchor_fp16_and_head_dim_64(mode, kernel):
+    """The anchored forms in fp16 and at head_dim 64: 4x4 blocks, radius 2, 3 query
+    frames against 6 KV frames (streaming rule) with the LQ anchor."""
+    spec = att._BlockGridSpec(f_cur=3, f_kv=6, h=16, w=24, block_t=3, bh=4, bw=4, rh=2, rw=2,
+                              rt=1, streaming=True)
+    g = _geom_of(spec)
+    L = 16 * 24
+    for dtype, d in ((torch.float16, 128), (torch.bfloat16, 64), (torch.float16, 64)):
+        print(f"[case] anchor {mode} {kernel} {dtype} d={d}", flush=True)
+        q = _rand((3 * L, 3, d), 51, d ** -0.5 * 4, dtype)
+        k = _rand((3 * L + 6 * L, 3, d), 52, d ** -0.5 * 4, dtype)
+        v = _rand((3 * L + 6 * L, 3, d), 53, 1.0, dtype)
+        out = _run_spec(spec, mode, q.to(DEV), k.to(DEV), v.to(DEV), kernel=kernel)
+        ref = obg.window_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), g, mode)
+        rel = metrics(out, ref)["rel_l2"]
+        assert rel < 4e-3, (mode, kernel, dtype, d, rel)
 
 
 def test_raise_paths():
