@@ -104,12 +104,17 @@ def rope_params(max_seq_len, dim, theta=10000.0):
     return torch.polar(torch.ones_like(ang), ang)
 
 
-def rope_table(cfg: SRDiTConfig, f, h, w, t_offset=0, device="cuda"):
+def rope_table(cfg: SRDiTConfig, f, h, w, t_offset=0, device="cuda", hw_stride=(1, 1)):
     """Per-token complex64 rotation [f*h*w, 1, head_dim/2] for a (f, h, w) grid.
 
     The frequency split follows rope_apply (models.py:176-178): c = head_dim/2
-    complex pairs split [c - 2(c//3), c//3, c//3] over (t, h, w).
+    complex pairs split [c - 2(c//3), c//3, c//3] over (t, h, w).  ``hw_stride``
+    (s_h, s_w) puts grid row i at position i*s_h and column j at j*s_w, as the
+    native LQ-anchor harvest does (models.py:1761-1785).
     """
+    s_h, s_w = (int(hw_stride[0]), int(hw_stride[1]))
+    if s_h < 1 or s_w < 1:
+        raise ValueError(f"rope_table: hw_stride must be >= 1, got {hw_stride!r}")
     d = cfg.head_dim
     dt, dh, dw = rope_axis_dims(d)
     c = d // 2
@@ -119,8 +124,8 @@ def rope_table(cfg: SRDiTConfig, f, h, w, t_offset=0, device="cuda"):
     assert ft.shape[1] + fh.shape[1] + fw.shape[1] == c
     tab = torch.cat([
         ft[t_offset:t_offset + f].view(f, 1, 1, -1).expand(f, h, w, -1),
-        fh[:h].view(1, h, 1, -1).expand(f, h, w, -1),
-        fw[:w].view(1, 1, w, -1).expand(f, h, w, -1)], dim=-1).reshape(f * h * w, 1, c)
+        fh[0:s_h * h:s_h].view(1, h, 1, -1).expand(f, h, w, -1),
+        fw[0:s_w * w:s_w].view(1, 1, w, -1).expand(f, h, w, -1)], dim=-1).reshape(f * h * w, 1, c)
     return tab.to(torch.complex64).to(device)
 
 
@@ -445,7 +450,7 @@ class SRDiT(nn.Module):
         return self._geometry(spec, lc, device, t_offset)
 
     def stream_geometry(self, f, h, w, lc, device, *, cached, chunk=3, t_offset=0,
-                        block_hw=(4, 4), block_radius_hw=(3, 3), anchor=None):
+                        block_hw=(4, 4), block_radius_hw=(3, 3), anchor=None, anchor_hw=None):
         """Geometry of one streaming chunk: ``f`` query frames against ``cached``
         cached frames plus themselves, under the reference's streaming rule with
         ``block_t = chunk`` and ``rt = f_kv // chunk - 1`` (attention.py:1575-1604
@@ -453,18 +458,23 @@ class SRDiT(nn.Module):
         sr_dit_5b.yaml:45-55).  ``anchor`` = "frame" / "chunk": the denoising
         steps' plan with the LQ anchor on the token grid (query frame i sees
         anchor frame i, or every query frame the whole anchor chunk;
-        attention.py:1520-1565, blockgrid_triton.py:117-133)."""
+        attention.py:1520-1565, blockgrid_triton.py:117-133).  ``anchor_hw``:
+        the anchor's own coarser token grid (the native LQ anchor,
+        causal_inference.py:725-752), None for the HR grid."""
         if anchor not in (None, "frame", "chunk"):
             raise ValueError(f"stream_geometry: anchor must be None, 'frame' or 'chunk', got {anchor!r}.")
         f_kv = int(cached) + f
+        a_hw = None
+        if anchor is not None and anchor_hw is not None and tuple(anchor_hw) != (h, w):
+            a_hw = (int(anchor_hw[0]), int(anchor_hw[1]))
         spec = att._BlockGridSpec(f_cur=f, f_kv=f_kv, h=h, w=w, block_t=chunk,
                                   bh=block_hw[0], bw=block_hw[1],
                                   rh=block_radius_hw[0], rw=block_radius_hw[1],
-                                  rt=max(f_kv // chunk - 1, 0), streaming=True)
+                                  rt=max(f_kv // chunk - 1, 0), streaming=True, anchor_hw=a_hw)
         return self._geometry(spec, lc, device, t_offset, anchor=anchor)
 
     def harvest_geometry(self, f, h, w, lc, device, *, per_frame=True, chunk=3, t_offset=0,
-                         block_hw=(4, 4), block_radius_hw=(3, 3)):
+                         block_hw=(4, 4), block_radius_hw=(3, 3), hw_stride=(1, 1)):
         """Geometry of the LQ-anchor harvest forward over ``f`` LQ frames, with no cache
         (causal_inference.py:426-508).  ``per_frame``: the reference runs each frame
         as its own one-frame sample at temporal offset ``t_offset + i``; every op but
@@ -472,7 +482,9 @@ class SRDiT(nn.Module):
         that frame (rt clamps to 0, attention.py:1598-1603), so this is one forward
         over the chunk at ``t_offset`` whose windows each see their own frame
         (``sym_rt = 0``).  Otherwise the whole chunk is one sample without a cache:
-        the non-streaming rule with ``block_t = chunk``."""
+        the non-streaming rule with ``block_t = chunk``.  ``hw_stride``: the
+        native LQ anchor's harvest runs on the LQ token grid (h, w) with RoPE at
+        HR positions (i * s_h, j * s_w)."""
         if per_frame:
             spec = att._BlockGridSpec(f_cur=f, f_kv=f, h=h, w=w, block_t=chunk,
                                       bh=block_hw[0], bw=block_hw[1],
@@ -483,14 +495,14 @@ class SRDiT(nn.Module):
                                       bh=block_hw[0], bw=block_hw[1],
                                       rh=block_radius_hw[0], rw=block_radius_hw[1],
                                       rt=max(f // chunk - 1, 0), streaming=False)
-        return self._geometry(spec, lc, device, t_offset)
+        return self._geometry(spec, lc, device, t_offset, hw_stride=hw_stride)
 
-    def _geometry(self, spec, lc, device, t_offset, anchor=None):
+    def _geometry(self, spec, lc, device, t_offset, anchor=None, hw_stride=(1, 1)):
         cfg = self.cfg
         f, h, w = spec.f_cur, spec.h, spec.w
-        rope = rope_table(cfg, f, h, w, t_offset, device)
+        rope = rope_table(cfg, f, h, w, t_offset, device, hw_stride=hw_stride)
         return {"grid": (f, h, w), "plan": bgh.cached_plan(spec, anchor_mode=anchor),
-                "anchor": anchor,
+                "anchor": anchor, "hw_stride": tuple(hw_stride),
                 "cross": CrossAttentionPlan(f * h * w, lc),
                 "rope": rope,
                 # (cos, sin) pairs [s, head_dim/2] for the fused RMSNorm + RoPE kernel

@@ -84,14 +84,18 @@ class StreamingRefiner:
     ("k") as models.py:638-643 does; a sequence gives one scale per
     denoising step, the last one repeating, as ``lq_guidance_scale`` does
     (causal_inference.py:904-906).  ``anchor_harvest_t`` is the harvest's
-    timestep (default ``context_noise``, :663-665).
+    timestep (default ``context_noise``, :663-665).  ``anchor_lq_hw`` (h_a, w_a):
+    the native LQ anchor ("true" scheme, causal_inference.py:725-752): the
+    harvest runs on the LQ token grid with RoPE at HR positions, and the
+    anchor keeps that coarser grid in attention; h and w must be multiples of
+    h_a and w_a.
     """
 
     def __init__(self, model, h, w, context_raw, *, chunk=3, kv_len=9,
                  step_list=(1000, 750, 500, 250), warp=True, context_noise=0,
                  sigma_start=1.0, shift=5.0, block_hw=(4, 4), block_radius_hw=(3, 3),
                  anchor=None, anchor_scale=1.0, anchor_mode="v", anchor_harvest_t=None,
-                 use_graph=True, seed=0, device="cuda", ring_cat=False):
+                 anchor_lq_hw=None, use_graph=True, seed=0, device="cuda", ring_cat=False):
         cfg = model.cfg
         if anchor not in (None, "frame", "chunk"):
             raise ValueError(f"anchor must be None, 'frame' or 'chunk', got {anchor!r}.")
@@ -106,6 +110,13 @@ class StreamingRefiner:
         self.anchor_scale = 1.0 if self._vary_scale else scales[0]
         self.harvest_t = float(int(context_noise if anchor_harvest_t is None else anchor_harvest_t))
         self.sigma_start = float(sigma_start)
+        self.anchor_hw = (h, w)
+        if anchor is not None and anchor_lq_hw is not None:
+            h_a, w_a = int(anchor_lq_hw[0]), int(anchor_lq_hw[1])
+            if h_a < 1 or w_a < 1 or h % h_a or w % w_a:
+                raise ValueError(f"StreamingRefiner: the native LQ anchor needs an integer token-grid "
+                                 f"ratio, HR {(h, w)} vs LQ {(h_a, w_a)}.")
+            self.anchor_hw = (h_a, w_a)
         self.model, self.h, self.w, self.chunk = model, h, w, chunk
         self.device = torch.device(device)
         self.block_hw, self.block_radius_hw = tuple(block_hw), tuple(block_radius_hw)
@@ -117,7 +128,7 @@ class StreamingRefiner:
         self.use_graph = use_graph
         self.ring_cat = bool(ring_cat)
         L = h * w
-        a_tok = chunk * L if anchor else 0
+        a_tok = chunk * self.anchor_hw[0] * self.anchor_hw[1] if anchor else 0
         self.rings = [KVRing(1, kv_len, chunk, L, cfg.num_heads, cfg.head_dim,
                              anchor_tokens=a_tok, device=self.device) for _ in model.blocks]
         self.gen = torch.Generator(device=self.device).manual_seed(seed)
@@ -128,6 +139,10 @@ class StreamingRefiner:
         # static inputs of the captured forwards
         self._lat = torch.zeros(cfg.in_dim, chunk, 2 * h, 2 * w, dtype=torch.float32,
                                 device=self.device)
+        self._lat_lq = self._lat
+        if self.anchor_hw != (h, w):
+            self._lat_lq = torch.zeros(cfg.in_dim, chunk, 2 * self.anchor_hw[0],
+                                       2 * self.anchor_hw[1], dtype=torch.float32, device=self.device)
         self._e = torch.zeros(1, cfg.dim, dtype=torch.float32, device=self.device)
         self._e0 = torch.zeros(1, 6, cfg.dim, dtype=torch.float32, device=self.device)
         self._geoms = {}
@@ -147,9 +162,13 @@ class StreamingRefiner:
                   block_radius_hw=self.block_radius_hw)
         args = (self.chunk, self.h, self.w, self.ctx.shape[0], self.device)
         if kind == "harvest":
-            return self.model.harvest_geometry(*args, per_frame=self.anchor == "frame", **kw)
+            h_a, w_a = self.anchor_hw
+            return self.model.harvest_geometry(self.chunk, h_a, w_a, self.ctx.shape[0], self.device,
+                                               per_frame=self.anchor == "frame",
+                                               hw_stride=(self.h // h_a, self.w // w_a), **kw)
         return self.model.stream_geometry(*args, cached=cached,
-                                          anchor=self.anchor if kind == "anchored" else None, **kw)
+                                          anchor=self.anchor if kind == "anchored" else None,
+                                          anchor_hw=self.anchor_hw, **kw)
 
     def _static_geom(self, key, t_offset):
         """The geometry for this forward kind and cache length, its RoPE table
@@ -160,7 +179,9 @@ class StreamingRefiner:
             g["t_offset"] = t_offset
             g["ring_cat"] = self.ring_cat
         elif g["t_offset"] != t_offset:
-            rope = rope_table(self.model.cfg, self.chunk, self.h, self.w, t_offset, self.device)
+            f, gh, gw = g["grid"]
+            rope = rope_table(self.model.cfg, f, gh, gw, t_offset, self.device,
+                              hw_stride=g["hw_stride"])
             g["rope"].copy_(rope)
             g["rope_cs"].copy_(torch.view_as_real(rope).reshape(g["rope_cs"].shape))
             g["t_offset"] = t_offset
@@ -186,9 +207,10 @@ class StreamingRefiner:
         """The harvest forward: every layer's K/V land in its ring's anchor prefix
         (the flow output is not used, as causal_inference.py:490-508 keeps only
         the caches), then the anchor scale (models.py:638-643)."""
-        s, dim = self.chunk * self.h * self.w, self.model.cfg.dim
+        s = self.chunk * self.anchor_hw[0] * self.anchor_hw[1]
+        dim = self.model.cfg.dim
         kv = [(r.anchor_k(0).view(s, dim), r.anchor_v(0).view(s, dim)) for r in self.rings]
-        out = self.model.forward_embedded(self._lat, self._e, self._e0, self.ctx, geom,
+        out = self.model.forward_embedded(self._lat_lq, self._e, self._e0, self.ctx, geom,
                                           cross=self.cross, kv_outs=kv)
         if self._vary_scale:
             for r, src in zip(self.rings, self._anchor_src):
@@ -203,7 +225,7 @@ class StreamingRefiner:
             e, e0 = self.model.time_embed(torch.tensor([float(t)], device=self.device))
             self._e.copy_(e)
             self._e0.copy_(e0)
-            self._lat.copy_(latent)
+            (self._lat_lq if key[0] == "harvest" else self._lat).copy_(latent)
             geom = self._static_geom(key, t_offset)
             self.forwards += 1
             if not self.use_graph:
@@ -230,7 +252,8 @@ class StreamingRefiner:
 
     def harvest(self, lq, t_offset):
         """LQ-anchor harvest of one chunk (causal_inference.py:426-508): ``lq``
-        [in_dim, chunk, 2h, 2w] (the upsampled LR latent), noised to
+        [in_dim, chunk, 2h, 2w] (the upsampled LR latent; with the native anchor
+        the LR latent itself, [in_dim, chunk, 2h_a, 2w_a]), noised to
         ``anchor_harvest_t`` when that is above 0, through the model at that
         timestep with no cache; each layer's K/V become its ring's anchor."""
         if self.anchor is None:
@@ -270,21 +293,23 @@ class StreamingRefiner:
         self.commit()
         return x0
 
-    def run(self, noise, t_offset=0, lq=None):
+    def run(self, noise, t_offset=0, lq=None, lq_anchor=None):
         """``noise`` [in_dim, F, 2h, 2w] with F a multiple of ``chunk``: refine every
         chunk in order; returns the refined latent [out_dim, F, 2h, 2w].  ``lq``
         (same shape): the upsampled LR latent; the first noisy input is then
         ``(1 - sigma_start) * lq + sigma_start * noise`` (causal_inference.py:667-668)
-        and each chunk's anchor is harvested from it."""
+        and each chunk's anchor is harvested from it, or from ``lq_anchor`` (the
+        native LR latent, [in_dim, F, 2h_a, 2w_a]) with the native anchor."""
         frames = noise.shape[1]
         if frames % self.chunk:
             raise ValueError(f"StreamingRefiner: {frames} frames is not a multiple of {self.chunk}.")
         if lq is not None and lq.shape != noise.shape:
             raise ValueError("StreamingRefiner.run: lq and noise must have the same shape.")
         noisy = noise if lq is None else (1.0 - self.sigma_start) * lq + self.sigma_start * noise
+        src = lq if lq_anchor is None else lq_anchor
         outs = []
         for c0 in range(0, frames, self.chunk):
             sl = slice(c0, c0 + self.chunk)
             outs.append(self.refine_chunk(noisy[:, sl], t_offset + c0,
-                                          None if lq is None else lq[:, sl]))
+                                          None if src is None else src[:, sl]))
         return torch.cat(outs, 1)

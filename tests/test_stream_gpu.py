@@ -177,3 +177,26 @@ def test_stream_per_step_anchor_scales(refiner_model):
         assert torch.equal(ring_e.anchor_v(0), (src.float() * 2.0).to(src.dtype))
         assert torch.equal(ring_e.anchor_k(0), ring_1.anchor_k(0))
     assert not torch.equal(e[0], one[0])
+
+
+@pytest.mark.parametrize("anchor", ["frame", "chunk"])
+def test_stream_native_lq_anchor(refiner_model, anchor):
+    """The native LQ anchor ("true" scheme, causal_inference.py:725-752): the harvest
+    runs on the 8x12 LQ token grid with RoPE at HR positions, the anchored steps read
+    the coarser anchor (anchor_hw); ring in place equals every layer reading the
+    concatenation, and graph replays equal eager forwards."""
+    noise, ctx, _ = _inputs(refiner_model.cfg, 3)
+    g = torch.Generator("cpu").manual_seed(9)
+    lqn = torch.randn(refiner_model.cfg.in_dim, 3 * CHUNK, 16, 24, generator=g).to(DEV)
+    kw = dict(anchor=anchor, anchor_lq_hw=(8, 12))
+    ra, a = _stream(refiner_model, noise, ctx, lq=lqn, use_graph=False, **kw)
+    rb, b = _stream(refiner_model, noise, ctx, lq=lqn, use_graph=False, ring_cat=True, **kw)
+    rg, gg = _stream(refiner_model, noise, ctx, lq=lqn, use_graph=True, **kw)
+    assert ra.rings[0].A == CHUNK * 8 * 12
+    for c, (x, y) in enumerate(zip(a, b)):
+        assert torch.isfinite(x).all()
+        assert torch.equal(x, y), f"chunk {c}"
+    for c, (x, y) in enumerate(zip(gg, a)):
+        err = (x - y).abs().max().item()
+        print(f"[metrics] native anchor {anchor} chunk {c}: max|graph - eager| = {err:.3e}", flush=True)
+        assert err <= 1e-3 * y.abs().max().item(), f"chunk {c}"

@@ -111,3 +111,33 @@ def test_streaming_refiner_anchor_arguments():
         StreamingRefiner(m, 8, 8, ctx, anchor="window", device="cpu")
     with pytest.raises(ValueError):
         StreamingRefiner(m, 8, 8, ctx, anchor="frame", anchor_mode="q", device="cpu")
+
+
+def test_rope_table_hw_stride_samples_the_hr_positions():
+    """The native anchor's harvest RoPE (models.py:1761-1785): grid row i at HR row
+    i*s_h, column j at HR column j*s_w; the temporal axis unchanged."""
+    from sr_dit.model import rope_table
+    cfg = SRDiTConfig()
+    full = rope_table(cfg, 2, 6, 12, t_offset=5, device="cpu").reshape(2, 6, 12, -1)
+    thin = rope_table(cfg, 2, 3, 4, t_offset=5, device="cpu", hw_stride=(2, 3)).reshape(2, 3, 4, -1)
+    assert torch.equal(thin, full[:, ::2, ::3])
+    with pytest.raises(ValueError):
+        rope_table(cfg, 1, 2, 2, device="cpu", hw_stride=(0, 1))
+
+
+@pytest.mark.parametrize("mode", ["frame", "chunk"])
+def test_native_anchor_stream_plan_matches_oracle(mode):
+    """Anchored steps with the native anchor grid: the plan's rows are the oracle's
+    for the same geometry with anchor_hw = the LQ token grid."""
+    import numpy as np
+    from oracle import blockgrid as obg
+    cfg = SRDiTConfig(dim=64, ffn_dim=128, num_heads=2, num_layers=0, in_dim=4, out_dim=4,
+                      text_dim=16, text_len=4)
+    geom = SRDiT(cfg).stream_geometry(3, 16, 24, 4, "cpu", cached=6, chunk=3, block_hw=(4, 4),
+                                      block_radius_hw=(2, 2), anchor=mode, anchor_hw=(8, 12))
+    plan = geom["plan"]
+    rows, block_m, m_tiles, hr_base, p_stride = obg.params_rows(obg.Geometry(
+        f_cur=3, f_kv=9, h=16, w=24, block_t=3, bh=4, bw=4, rh=2, rw=2, rt=2, streaming=True,
+        anchor_hw=(8, 12)), mode)
+    assert np.array_equal(plan["params"].numpy(), np.asarray(rows, dtype=np.int64))
+    assert plan["hr_base"] == hr_base == 3 * 8 * 12 and plan["p_stride"] == p_stride
