@@ -88,14 +88,17 @@ class StreamingRefiner:
     the native LQ anchor ("true" scheme, causal_inference.py:725-752): the
     harvest runs on the LQ token grid with RoPE at HR positions, and the
     anchor keeps that coarser grid in attention; h and w must be multiples of
-    h_a and w_a.
+    h_a and w_a.  ``anchor_native_scheme`` "repeat" instead copies every LQ
+    token into its s_h x s_w HR block (causal_inference.py:104-140) and
+    attends the anchor on the HR grid.
     """
 
     def __init__(self, model, h, w, context_raw, *, chunk=3, kv_len=9,
                  step_list=(1000, 750, 500, 250), warp=True, context_noise=0,
                  sigma_start=1.0, shift=5.0, block_hw=(4, 4), block_radius_hw=(3, 3),
                  anchor=None, anchor_scale=1.0, anchor_mode="v", anchor_harvest_t=None,
-                 anchor_lq_hw=None, use_graph=True, seed=0, device="cuda", ring_cat=False):
+                 anchor_lq_hw=None, anchor_native_scheme="true", use_graph=True, seed=0,
+                 device="cuda", ring_cat=False):
         cfg = model.cfg
         if anchor not in (None, "frame", "chunk"):
             raise ValueError(f"anchor must be None, 'frame' or 'chunk', got {anchor!r}.")
@@ -110,13 +113,18 @@ class StreamingRefiner:
         self.anchor_scale = 1.0 if self._vary_scale else scales[0]
         self.harvest_t = float(int(context_noise if anchor_harvest_t is None else anchor_harvest_t))
         self.sigma_start = float(sigma_start)
-        self.anchor_hw = (h, w)
+        if anchor_native_scheme not in ("true", "repeat"):
+            raise ValueError(f"anchor_native_scheme must be 'true' or 'repeat', got "
+                             f"{anchor_native_scheme!r}.")
+        self.anchor_hw = (h, w)     # the harvest's token grid
+        self._repeat = False        # the harvest grid is expanded to the HR grid
         if anchor is not None and anchor_lq_hw is not None:
             h_a, w_a = int(anchor_lq_hw[0]), int(anchor_lq_hw[1])
             if h_a < 1 or w_a < 1 or h % h_a or w % w_a:
                 raise ValueError(f"StreamingRefiner: the native LQ anchor needs an integer token-grid "
                                  f"ratio, HR {(h, w)} vs LQ {(h_a, w_a)}.")
             self.anchor_hw = (h_a, w_a)
+            self._repeat = anchor_native_scheme == "repeat" and (h_a, w_a) != (h, w)
         self.model, self.h, self.w, self.chunk = model, h, w, chunk
         self.device = torch.device(device)
         self.block_hw, self.block_radius_hw = tuple(block_hw), tuple(block_radius_hw)
@@ -128,7 +136,8 @@ class StreamingRefiner:
         self.use_graph = use_graph
         self.ring_cat = bool(ring_cat)
         L = h * w
-        a_tok = chunk * self.anchor_hw[0] * self.anchor_hw[1] if anchor else 0
+        grid_a = (h, w) if self._repeat else self.anchor_hw  # the anchor's grid in attention
+        a_tok = chunk * grid_a[0] * grid_a[1] if anchor else 0
         self.rings = [KVRing(1, kv_len, chunk, L, cfg.num_heads, cfg.head_dim,
                              anchor_tokens=a_tok, device=self.device) for _ in model.blocks]
         self.gen = torch.Generator(device=self.device).manual_seed(seed)
@@ -149,6 +158,13 @@ class StreamingRefiner:
         self._graphs = {}
         self.forwards = 0
         self._anchor_src = None
+        self._lq_kv = None
+        if self._repeat:  # the harvest's K/V on the LQ grid, expanded after the forward
+            n_lq = chunk * self.anchor_hw[0] * self.anchor_hw[1]
+            self._lq_kv = [(torch.empty(n_lq, cfg.num_heads, cfg.head_dim, dtype=r.k.dtype,
+                                        device=self.device),
+                            torch.empty(n_lq, cfg.num_heads, cfg.head_dim, dtype=r.v.dtype,
+                                        device=self.device)) for r in self.rings]
         if self._vary_scale:
             self._anchor_src = [torch.empty_like(self._scaled_part(r)) for r in self.rings]
             self._scale_dev = torch.ones(1, dtype=torch.float32, device=self.device)
@@ -168,7 +184,7 @@ class StreamingRefiner:
                                                hw_stride=(self.h // h_a, self.w // w_a), **kw)
         return self.model.stream_geometry(*args, cached=cached,
                                           anchor=self.anchor if kind == "anchored" else None,
-                                          anchor_hw=self.anchor_hw, **kw)
+                                          anchor_hw=None if self._repeat else self.anchor_hw, **kw)
 
     def _static_geom(self, key, t_offset):
         """The geometry for this forward kind and cache length, its RoPE table
@@ -209,9 +225,20 @@ class StreamingRefiner:
         the caches), then the anchor scale (models.py:638-643)."""
         s = self.chunk * self.anchor_hw[0] * self.anchor_hw[1]
         dim = self.model.cfg.dim
-        kv = [(r.anchor_k(0).view(s, dim), r.anchor_v(0).view(s, dim)) for r in self.rings]
+        if self._repeat:
+            kv = [(k.view(s, dim), v.view(s, dim)) for k, v in self._lq_kv]
+        else:
+            kv = [(r.anchor_k(0).view(s, dim), r.anchor_v(0).view(s, dim)) for r in self.rings]
         out = self.model.forward_embedded(self._lat_lq, self._e, self._e0, self.ctx, geom,
                                           cross=self.cross, kv_outs=kv)
+        if self._repeat:  # LQ (i, j) -> HR (s_h i .. s_h i + s_h - 1, s_w j .. s_w j + s_w - 1)
+            f, (h_a, w_a) = self.chunk, self.anchor_hw
+            s_h, s_w = self.h // h_a, self.w // w_a
+            for r, (k, v) in zip(self.rings, self._lq_kv):
+                for src, dst in ((k, r.anchor_k(0)), (v, r.anchor_v(0))):
+                    n, d = src.shape[1], src.shape[2]
+                    dst.view(f, h_a, s_h, w_a, s_w, n, d).copy_(
+                        src.view(f, h_a, 1, w_a, 1, n, d).expand(f, h_a, s_h, w_a, s_w, n, d))
         if self._vary_scale:
             for r, src in zip(self.rings, self._anchor_src):
                 src.copy_(self._scaled_part(r))

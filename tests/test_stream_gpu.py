@@ -200,3 +200,37 @@ def test_stream_native_lq_anchor(refiner_model, anchor):
         err = (x - y).abs().max().item()
         print(f"[metrics] native anchor {anchor} chunk {c}: max|graph - eager| = {err:.3e}", flush=True)
         assert err <= 1e-3 * y.abs().max().item(), f"chunk {c}"
+
+
+def test_stream_native_anchor_repeat_scheme(refiner_model):
+    """Native anchor, "repeat" scheme (causal_inference.py:104-140): the harvested LQ
+    K/V, copied into s_h x s_w HR blocks, become an HR-grid anchor; it equals the
+    nearest-neighbour expansion of the "true" scheme's anchor; ring in place equals
+    the concatenation and graph replays equal eager forwards."""
+    noise, ctx, _ = _inputs(refiner_model.cfg, 2)
+    g = torch.Generator("cpu").manual_seed(11)
+    lqn = torch.randn(refiner_model.cfg.in_dim, 2 * CHUNK, 16, 24, generator=g).to(DEV)
+
+    def make(**kw):
+        return StreamingRefiner(refiner_model, H, W, ctx, chunk=CHUNK, kv_len=KV, seed=1,
+                                device=DEV, use_graph=False, anchor="frame",
+                                anchor_lq_hw=(8, 12), **kw)
+    rt, rr = make(), make(anchor_native_scheme="repeat")
+    print("[case] native repeat harvest", flush=True)
+    rt.harvest(lqn[:, :CHUNK], 0)
+    rr.harvest(lqn[:, :CHUNK], 0)
+    torch.cuda.synchronize()
+    for a, b in zip(rt.rings, rr.rings):
+        assert b.A == CHUNK * H * W
+        for lq_t, hr_t in ((a.anchor_k(0), b.anchor_k(0)), (a.anchor_v(0), b.anchor_v(0))):
+            n, d = lq_t.shape[1], lq_t.shape[2]
+            want = lq_t.view(CHUNK, 8, 1, 12, 1, n, d).expand(CHUNK, 8, 2, 12, 2, n, d)
+            assert torch.equal(hr_t.view(CHUNK, 8, 2, 12, 2, n, d), want)
+    kw = dict(anchor="frame", anchor_lq_hw=(8, 12), anchor_native_scheme="repeat")
+    ra, a = _stream(refiner_model, noise, ctx, lq=lqn, use_graph=False, **kw)
+    rb, b = _stream(refiner_model, noise, ctx, lq=lqn, use_graph=False, ring_cat=True, **kw)
+    rg, gg = _stream(refiner_model, noise, ctx, lq=lqn, use_graph=True, **kw)
+    for c, (x, y) in enumerate(zip(a, b)):
+        assert torch.equal(x, y), f"chunk {c}"
+    for c, (x, y) in enumerate(zip(gg, a)):
+        assert (x - y).abs().max().item() <= 1e-3 * y.abs().max().item(), f"chunk {c}"
