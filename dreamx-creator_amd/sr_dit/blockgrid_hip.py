@@ -17,6 +17,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from . import kv_share
 
 # Params row layouts (int32, one row per window); the kernel reads them with
 # raw pointer arithmetic.  All lengths are lengths, not end indices.
@@ -165,6 +166,16 @@ def mean_kv_tokens(plan) -> float:
 #: and 1024 context tokens: 193 vs 202 us and 315 vs 318 us; 2048: 556 vs 539 us;
 #: inside the full refiner step the two forms tie).
 GROUPED_MIN_KV = 1536
+
+
+#: ``kernel="auto"`` leaves the shared-fetch kernel off: in interleaved A/B runs
+#: on one MI355X it is slower than the one-member grouped kernel on c2-c4
+#: (c3: 455 us with two members, 515 us with four, against 402 us), though it
+#: moves half the K/V bytes: the barrier couples 4-8 wavefronts per step and
+#: the step control costs more SALU/VALU per MFMA.  ``kernel="shared"``
+#: (four members) and ``"shared2"`` (two) select it.
+SHARED_AUTO = False
+SHARED_MEMBERS = 2
 
 
 def launch_order(plan) -> torch.Tensor:
@@ -324,6 +335,26 @@ def paired_fraction(groups: torch.Tensor) -> float:
     return 2 * paired / (2 * paired + (n - paired))
 
 
+def _share_tables(plan, H, W, head_dim, device, members):
+    """The shared-fetch schedule of ``plan`` on ``device`` (built and copied once),
+    or None when the plan is not made of 4x8-token KV units."""
+    key = ("share", H, W, head_dim, members)
+    host = plan.get(key)
+    if host is None:
+        host = plan[key] = (kv_share.build_share_schedule(plan, H, W, members)
+                            if kv_share.share_supported(plan, H, W, head_dim) else False)
+    if host is False:
+        return None
+    dkey = ("share_dev", H, W, head_dim, members, device)
+    dev = plan.get(dkey)
+    if dev is None:
+        dev = plan[dkey] = {"groups": host["groups"].to(device),
+                            "step_off": host["step_off"].to(device),
+                            "steps": host["steps"].to(device), "n_groups": host["n_groups"],
+                            "members": host["members"]}
+    return dev
+
+
 def _device_tables(plan, device):
     """(params, order) on ``device``, copied once per plan and device."""
     key = ("dev", device)
@@ -391,9 +422,22 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     mode = 1 if anchor_mode == "frame" else 0
     if (plan["p_stride"] == P_FRAME) != (mode == 1):
         raise ValueError("run_blockgrid_hip: plan layout does not match anchor_mode.")
-    if kernel not in ("auto", "grouped", "solo", "single"):
-        raise ValueError("run_blockgrid_hip: kernel must be auto, grouped, solo or single, got "
-                         f"{kernel!r}")
+    if kernel not in ("auto", "shared", "shared2", "grouped", "solo", "single"):
+        raise ValueError("run_blockgrid_hip: kernel must be auto, shared, shared2, grouped, solo "
+                         f"or single, got {kernel!r}")
+    if kernel in ("auto", "shared", "shared2"):
+        members = 2 if kernel == "shared2" else (SHARED_MEMBERS if kernel == "auto" else 4)
+        share = (_share_tables(plan, h, w, d, q.device, members)
+                 if anchor_mode is None and plan["p_stride"] == P_PLAIN else None)
+        if share is not None and (kernel != "auto" or SHARED_AUTO):
+            _lib.window_attn_shared_fwd(
+                q, k_ext, v_ext, out, params, share, n_w=plan["n_w"], hr_base=hr_base, H=h, W=w,
+                n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0], scale=d ** -0.5, ring=ring,
+                amax_out=amax_out)
+            return out
+        if kernel != "auto":
+            raise ValueError("run_blockgrid_hip: the shared-fetch kernel needs plain rows without "
+                             "an anchor, head_dim 128 and KV cuboids made of 4x8-token units.")
     if kernel == "grouped" and not groups_supported(plan):
         raise ValueError("run_blockgrid_hip: the grouped kernel needs plain rows without an anchor.")
     if kernel == "solo" and not solo_supported(plan):
