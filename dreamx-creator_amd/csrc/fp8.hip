@@ -27,6 +27,9 @@
 #include "common.h"
 #include "fp8_common.h"
 
+#include <type_traits>
+#include <utility>
+
 namespace srdit {
 namespace {
 
@@ -162,9 +165,6 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const T* __restrict__
 // ---------------------------------------------------------------------- GEMM
 
 constexpr int GT = 256;                       // tile rows (M) and columns (N)
-constexpr int GK = 128;                       // K bytes per stage
-constexpr int G_OPERAND_BYTES = GT * GK;      // 32 KB per operand per stage
-constexpr int G_STAGE_BYTES = 2 * G_OPERAND_BYTES;
 constexpr int G_GROUP_M = 8;                  // M tiles per raster group
 
 struct GemmArgs {
@@ -182,6 +182,16 @@ struct GemmArgs {
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void compiler_fence_gemm() { asm volatile("" ::: "memory"); }
+
+// Wait until at most N vector-memory operations of this wavefront are in
+// flight (its newest fills), and for all its LDS reads.
+template <int N>
+__device__ __forceinline__ void waitcnt_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
 
 __device__ __forceinline__ i32x8_t read_frag(const uint8_t* lds, int off_lo, int off_hi) {
   const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(lds + off_lo);
@@ -245,120 +255,30 @@ __global__ __launch_bounds__(256) void gelu_amax_kernel(const uint16_t* x, int64
   if (threadIdx.x == 0) atomicMax(amax_ws, max(max(part[0], part[1]), max(part[2], part[3])));
 }
 
+// The epilogue of one wavefront's NI x NJ blocks of 32 x 32: acc[i][j] is
+// out^T[n-subtile i][m-subtile j] (the weight is the MFMA A operand); lane l
+// holds row m = m_base + 32 j + (l & 31) and columns n = n_base + 32 i + 8 (r/4)
+// + 4 (l/32) + r%4, stored as 8-byte runs of four bf16.
 // EPI 0: out = bf16(v); EPI 1: out = bf16(gelu(bf16(v))), the Linear's bf16
 // output fed to nn.GELU(approximate='tanh').  AMAX: also the max |out| (float
 // bits) of the whole output into *g.amax_out, for a per-tensor quantiser.
-template <int EPI, bool AMAX>
-__global__ __launch_bounds__(256) void fp8_gemm_kernel(const GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G_STAGE_BYTES];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
-
-  // Tile raster: XCD-contiguous task ranges, then groups of G_GROUP_M tile rows
-  // walked column by column so the workgroups sharing an L2 share A and B tiles.
-  const uint32_t n_tasks = (uint32_t)g.tiles_m * g.tiles_n;
-  const uint32_t task = xcd_task(blockIdx.x, n_tasks);
-  const int width = G_GROUP_M * g.tiles_n;
-  const int group = task / width;
-  const int first_m = group * G_GROUP_M;
-  const int gsize = min(g.tiles_m - first_m, G_GROUP_M);
-  const int tm = first_m + (int)(task % width) % gsize;
-  const int tn = (int)(task % width) / gsize;
-  const int m0 = tm * GT, n0 = tn * GT;
-
-  // Buffer descriptors over this tile's rows to the end of each operand:
-  // reads of rows >= M (or N) fall outside num_records and return zero.
-  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(g.a + (int64_t)m0 * g.K), 0, (g.M - m0) * g.K, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(g.b + (int64_t)n0 * g.K), 0, (g.N - n0) * g.K, 0x00020000);
-
-  // Fill mapping: instruction q = wave*8 + j writes LDS bytes [q*1024, +1024),
-  // lane l -> tile row q*8 + l/8, chunk position l%8, which holds source chunk
-  // (l%8) ^ ((row >> 1) & 7) = (l%8) ^ ((4*(j&1) + (l>>4)) & 7).
-  const int frow = wave * 64 + (lane >> 3);
-  const int fpos = lane & 7;
-  const int fchunk0 = fpos ^ ((lane >> 4) & 7);
-  const int fchunk1 = fpos ^ ((4 + (lane >> 4)) & 7);
-  const int fvoff0 = frow * g.K + fchunk0 * 16;
-  const int fvoff1 = frow * g.K + fchunk1 * 16;
-
-  auto fill = [&](int stage, int kt) {
-    uint8_t* base = smem + stage * G_STAGE_BYTES + wave * 8192;
-    const int koff = kt * GK;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int voff = ((j & 1) ? fvoff1 : fvoff0) + j * 8 * g.K;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (lds_void_t*)(base + j * 1024), 16, voff,
-                                               koff, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs_b, (lds_void_t*)(base + G_OPERAND_BYTES + j * 1024), 16, voff, koff, 0, 0);
-    }
-  };
-
-  // Operand read offsets: row (l & 31) of a 32-row subtile, chunks
-  // kk*4 + (l>>5)*2 + h at position chunk ^ ((l & 31) >> 1 & 7).
-  const int rrow = lane & 31;
-  const int rswz = (rrow >> 1) & 7;
-  int roff[2][2];
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      roff[kk][h] = rrow * GK + (((kk * 4 + (lane >> 5) * 2 + h) ^ rswz) * 16);
-
-  f32x16_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  const int nk = g.K / GK;
-  fill(0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_s_barrier();
-    if (kt + 1 < nk) fill((kt + 1) & 1, kt + 1);
-    const uint8_t* sa_ = smem + (kt & 1) * G_STAGE_BYTES;               // activation tile
-    const uint8_t* sb_ = sa_ + G_OPERAND_BYTES;                          // weight tile
-    const uint8_t* ta = sa_ + wm * 128 * GK;
-    const uint8_t* tb = sb_ + wn * 128 * GK;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      i32x8_t fw[4], fx[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fw[i] = read_frag(tb + i * 32 * GK, roff[kk][0], roff[kk][1]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) fx[j] = read_frag(ta + j * 32 * GK, roff[kk][0], roff[kk][1]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[i], fx[j], acc[i][j], 0, 0,
-                                                                      0, 0, 0, 0);
-    }
-  }
-
-  // Epilogue: acc[i][j] is the 32 x 32 block out^T[n-subtile i][m-subtile j];
-  // lane l holds row m = .. + (l & 31) and columns n = .. + 8*(r/4) + 4*(l/32) + r%4.
+template <int EPI, bool AMAX, int NI, int NJ>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16_t (&acc)[NI][NJ],
+                                              int m_base, int n_base, int lane) {
   const int mrow = lane & 31;
   const int ncol = 4 * (lane >> 5);
   uint32_t amax = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + wm * 128 + j * 32 + mrow;
+  for (int j = 0; j < NJ; ++j) {
+    const int m = m_base + j * 32 + mrow;
     if (m >= g.M) continue;
     const float sa = g.sa[g.sa_per_row ? m : 0];
     uint16_t* orow = g.out + (int64_t)m * g.ldo;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NI; ++i) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * 128 + i * 32 + 8 * q + ncol;
+        const int n = n_base + i * 32 + 8 * q + ncol;
         if (n >= g.N) continue;
         float sb[4], bias[4];
         if (g.sb_per_col) {
@@ -406,6 +326,132 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(const GemmArgs g) {
     for (int o = 32; o > 0; o >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, o));
     if (lane == 0) atomicMax(g.amax_out, amax);
   }
+}
+
+// The fp8 GEMM: a 256 x 256 output tile per workgroup of eight wavefronts
+// (two per SIMD); wavefront (wm, wn) = (w & 1, w >> 1) owns activation rows
+// [128 wm, +128) and weight rows [64 wn, +64), 2 x 4 blocks of
+// v_mfma_f32_32x32x64_f8f6f4 (128 accumulator registers).  K advances 128
+// bytes per stage (whole 128-byte lines per fill row) through a two-stage
+// 2 x 64 KB LDS ring filled one stage ahead by buffer_load ... lds; each stage
+// runs two 64-byte MFMA depths.  LDS rows are 128 bytes; chunk c of row r
+// sits at c ^ ((r >> 1) & 7), so the fragment reads of 16 lanes cover all 64
+// banks.  Measured against alternatives on one MI355X (21600 x 3072 x 3072,
+// per-tensor scales): 64-byte stages in a four-stage ring filled three or
+// four ahead, 4 wavefronts of 128 x 128, register-staged fills and
+// double-buffered fragments were all equal or slower (1.43-1.80 PFLOP/s
+// against 1.79-1.87); without its fills this kernel runs 2.56 PFLOP/s, so the
+// L2 -> LDS fills, not the MFMA issue, bound it.
+constexpr int QK = 128;
+constexpr int Q_OPB = GT * QK;             // 32 KB per operand per stage
+constexpr int Q_STAGE = 2 * Q_OPB;
+
+template <int EPI, bool AMAX>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fp8_gemm_wide_kernel(const GemmArgs g) {
+  constexpr int NI = 2, NJ = 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * Q_STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+
+  const uint32_t n_tasks = (uint32_t)g.tiles_m * g.tiles_n;
+  const uint32_t task = xcd_task(blockIdx.x, n_tasks);
+  const int width = G_GROUP_M * g.tiles_n;
+  const int group = task / width;
+  const int first_m = group * G_GROUP_M;
+  const int gsize = min(g.tiles_m - first_m, G_GROUP_M);
+  const int tm = first_m + (int)(task % width) % gsize;
+  const int tn = (int)(task % width) / gsize;
+  const int m0 = tm * GT, n0 = tn * GT;
+
+  auto rsrc_of = [](const uint8_t* p, int64_t bytes) __attribute__((always_inline)) -> i32x4_t {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    return i32x4_t{static_cast<int>(static_cast<uint32_t>(a)),
+                   static_cast<int>(static_cast<uint32_t>(a >> 32)), static_cast<int>(bytes),
+                   0x00020000};
+  };
+  const i32x4_t rs_a = rsrc_of(g.a + (int64_t)m0 * g.K, (int64_t)(g.M - m0) * g.K);
+  const i32x4_t rs_b = rsrc_of(g.b + (int64_t)n0 * g.K, (int64_t)(g.N - n0) * g.K);
+
+  // Fill: wavefront w writes rows [32 w, +32) of both tiles in four 1 KB loads
+  // (8 rows of 128 bytes); lane l -> row 8 q + l/8, position l%8, holding
+  // source chunk (l%8) ^ ((row >> 1) & 7) = (l%8) ^ ((4 (q & 1) + (l >> 4)) & 7).
+  const int fpos = lane & 7;
+  const int fbase = (wave * 32 + (lane >> 3)) * g.K;
+  const int fv_even = fbase + ((fpos ^ ((lane >> 4) & 7)) * 16);
+  const int fv_odd = fbase + ((fpos ^ ((4 + (lane >> 4)) & 7)) * 16);
+  const int frow8 = 8 * g.K;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * 32 * QK;
+  auto dma = [](i32x4_t rsrc, int voff, int soff, uint32_t lds) __attribute__((always_inline)) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
+                 "{m0}"(lds)
+                 : "memory");
+  };
+  auto fill = [&](int stage, int kt) __attribute__((always_inline)) {
+    const uint32_t base = lds0 + stage * Q_STAGE;
+    const int koff = kt * QK;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      dma(rs_a, ((q & 1) ? fv_odd : fv_even) + q * frow8, koff, base + q * 1024);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      dma(rs_b, ((q & 1) ? fv_odd : fv_even) + q * frow8, koff, base + Q_OPB + q * 1024);
+  };
+
+  const int rrow = lane & 31;
+  const int rswz = (rrow >> 1) & 7;
+  const int h2 = 2 * (lane >> 5);
+  int roff[2][2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) roff[kk][h] = rrow * QK + (((kk * 4 + h2 + h) ^ rswz) * 16);
+
+  f32x16_t acc[NI][NJ];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16_t{};
+  struct Frags {
+    i32x8_t w[NI], x[NJ];
+  };
+  auto read_sub = [&](int st, auto kk_c) __attribute__((always_inline)) -> Frags {
+    constexpr int kk = decltype(kk_c)::value;
+    const uint8_t* ta = smem + st * Q_STAGE + wm * 128 * QK;
+    const uint8_t* tb = smem + st * Q_STAGE + Q_OPB + wn * 64 * QK;
+    Frags f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) f.w[i] = read_frag(tb + i * 32 * QK, roff[kk][0], roff[kk][1]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) f.x[j] = read_frag(ta + j * 32 * QK, roff[kk][0], roff[kk][1]);
+    return f;
+  };
+  auto mma = [&](const Frags& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[i], f.x[j], acc[i][j], 0,
+                                                                    0, 0, 0, 0, 0);
+  };
+
+  const int nk = g.K / QK;
+  fill(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    compiler_fence_gemm();
+    waitcnt_vm<0>();
+    __builtin_amdgcn_s_barrier();
+    compiler_fence_gemm();
+    const int st = kt & 1;
+    if (kt + 1 < nk) fill(st ^ 1, kt + 1);
+    const Frags f0 = read_sub(st, std::integral_constant<int, 0>{});
+    const Frags f1 = read_sub(st, std::integral_constant<int, 1>{});
+    mma(f0);
+    mma(f1);
+  }
+  gemm_epilogue<EPI, AMAX, NI, NJ>(g, acc, m0 + wm * 128, n0 + wn * 64, lane);
 }
 
 template <typename Launch>
@@ -528,11 +574,11 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
     SRDIT_LAUNCH_CHECK("clear_u32_kernel");
   }
   const unsigned grid = (unsigned)tiles;
-  if (epilogue == 0 && !amax_out) fp8_gemm_kernel<0, false><<<grid, 256, 0, s>>>(g);
-  else if (epilogue == 0) fp8_gemm_kernel<0, true><<<grid, 256, 0, s>>>(g);
-  else if (!amax_out) fp8_gemm_kernel<1, false><<<grid, 256, 0, s>>>(g);
-  else fp8_gemm_kernel<1, true><<<grid, 256, 0, s>>>(g);
-  SRDIT_LAUNCH_CHECK("fp8_gemm_kernel");
+  if (epilogue == 0 && !amax_out) fp8_gemm_wide_kernel<0, false><<<grid, 512, 0, s>>>(g);
+  else if (epilogue == 0) fp8_gemm_wide_kernel<0, true><<<grid, 512, 0, s>>>(g);
+  else if (!amax_out) fp8_gemm_wide_kernel<1, false><<<grid, 512, 0, s>>>(g);
+  else fp8_gemm_wide_kernel<1, true><<<grid, 512, 0, s>>>(g);
+  SRDIT_LAUNCH_CHECK("fp8_gemm_wide_kernel");
   return SRDIT_OK;
 }
 }  // namespace
