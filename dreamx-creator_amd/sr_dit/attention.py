@@ -28,6 +28,8 @@ reference code path is unchanged when it is absent.
 """
 from __future__ import annotations
 
+import warnings
+
 from typing import NamedTuple
 
 import torch
@@ -462,29 +464,46 @@ def prewarm_blockgrid_hip(*, h, w, bt, bh, bw, rh, rw, n, d, variants,
                           dtype=torch.bfloat16, anchor_hw=None):
     """Counterpart of ``prewarm_blockgrid_triton`` (attention.py:883-961).
 
-    The HIP kernels are compiled ahead of time, so there is nothing to JIT;
-    this builds and uploads the plans the caller will use and returns the
-    variants prepared (``[]`` when no GPU is present), keeping the signature
-    and return contract.
+    The HIP kernels are compiled ahead of time, so nothing is JIT-compiled;
+    each ``(f_cur, anchor_mode)`` variant is still launched once on zero
+    tensors of the production geometry, which builds its plan, uploads the
+    plan's device tables (params, launch order, member tables) and pays the
+    first launch before inference.  Same signature and return contract: the
+    variants warmed, ``[]`` without a GPU; a variant the planner or the
+    launcher rejects is skipped with a warning, never raised.
     """
     if not torch.cuda.is_available():
         return []
     dev = torch.device(device if device is not None else "cuda")
     if dev.type != "cuda":
         return []
-    warmed = []
     a_hw = (None if anchor_hw is None or (int(anchor_hw[0]), int(anchor_hw[1])) == (h, w)
             else (int(anchor_hw[0]), int(anchor_hw[1])))
+    hw = int(h) * int(w)
+    hw_a = hw if a_hw is None else a_hw[0] * a_hw[1]
+    warmed = []
     for f_cur, anchor_mode in variants:
-        f_cur = int(f_cur)
-        fkv = int(f_kv) if f_kv is not None else max(f_cur, int(bt))
-        spec = _BlockGridSpec(
-            f_cur=f_cur, f_kv=fkv, h=h, w=w, block_t=int(bt),
-            bh=int(bh), bw=int(bw), rh=int(rh), rw=int(rw),
-            hist=(None if block_radius_t is None else (2 * int(block_radius_t) + 1) * int(bt)),
-            rt=max(0, fkv // int(bt) - 1), chunk_frames=None,
-            streaming=True, anchor_hw=a_hw)
-        plan = _bgh.cached_plan(spec, anchor_mode=anchor_mode)
-        _bgh._device_tables(plan, dev)
-        warmed.append((f_cur, anchor_mode))
+        try:
+            if anchor_mode not in (None, "frame", "chunk"):
+                raise ValueError(f"anchor_mode must be None, 'frame' or 'chunk', got {anchor_mode!r}")
+            f_cur = int(f_cur)
+            fkv = int(f_kv) if f_kv is not None else max(f_cur, int(bt))
+            spec = _BlockGridSpec(
+                f_cur=f_cur, f_kv=fkv, h=h, w=w, block_t=int(bt),
+                bh=int(bh), bw=int(bw), rh=int(rh), rw=int(rw),
+                hist=(None if block_radius_t is None else (2 * int(block_radius_t) + 1) * int(bt)),
+                rt=max(0, fkv // int(bt) - 1), chunk_frames=None,
+                streaming=True, anchor_hw=a_hw)
+            plan = _bgh.cached_plan(spec, anchor_mode=anchor_mode)
+            n_anchor = f_cur * hw_a if anchor_mode is not None else 0
+            q = torch.zeros(f_cur * hw, n, d, device=dev, dtype=dtype)
+            kv = torch.zeros(n_anchor + fkv * hw, n, d, device=dev, dtype=dtype)
+            _bgh.run_blockgrid_hip(q, kv, kv, torch.empty_like(q), plan=plan, f_cur=f_cur, h=h,
+                                   w=w, n=n, d=d, anchor_mode=anchor_mode)
+            warmed.append((f_cur, anchor_mode))
+        except (RuntimeError, ValueError, TypeError) as e:
+            warnings.warn(f"prewarm_blockgrid_hip: variant (f_cur={f_cur}, "
+                          f"anchor_mode={anchor_mode!r}) skipped: {type(e).__name__}: {e}")
+    if warmed:
+        torch.cuda.synchronize(dev)
     return warmed
