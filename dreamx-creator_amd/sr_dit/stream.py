@@ -85,19 +85,26 @@ class StreamingRefiner:
     denoising step, the last one repeating, as ``lq_guidance_scale`` does
     (causal_inference.py:904-906).  ``anchor_harvest_t`` is the harvest's
     timestep (default ``context_noise``, :663-665).  ``anchor_lq_hw`` (h_a, w_a):
-    the native LQ anchor ("true" scheme, causal_inference.py:725-752): the
-    harvest runs on the LQ token grid with RoPE at HR positions, and the
-    anchor keeps that coarser grid in attention; h and w must be multiples of
-    h_a and w_a.  ``anchor_native_scheme`` "repeat" instead copies every LQ
-    token into its s_h x s_w HR block (causal_inference.py:104-140) and
-    attends the anchor on the HR grid.
+    the native LQ anchor, harvested on the LQ token grid with RoPE at HR
+    positions; h and w must be multiples of h_a and w_a.  Its
+    ``anchor_native_scheme`` is the reference's default "repeat"
+    (causal_inference.py:650, inference_sr.py:295): every LQ token's K/V is
+    copied into its s_h x s_w HR block (causal_inference.py:104-140) and the
+    anchor is attended on the HR grid; "true" (causal_inference.py:725-752)
+    keeps the coarser grid in attention, which lowers the anchor's softmax
+    mass by about s_h*s_w against what the anchor LoRA was distilled with.
+
+    ``sigma_start`` defaults to the shipped 0.6251 (sr_dit_5b.yaml:65,
+    run_inference.sh:38): the warped step list 1000/937.5/833.3/625 keeps the
+    single step t=625, so an anchored chunk is three forwards (harvest, step,
+    refresh); 1.0 keeps all four steps.
     """
 
     def __init__(self, model, h, w, context_raw, *, chunk=3, kv_len=9,
                  step_list=(1000, 750, 500, 250), warp=True, context_noise=0,
-                 sigma_start=1.0, shift=5.0, block_hw=(4, 4), block_radius_hw=(3, 3),
+                 sigma_start=0.6251, shift=5.0, block_hw=(4, 4), block_radius_hw=(3, 3),
                  anchor=None, anchor_scale=1.0, anchor_mode="v", anchor_harvest_t=None,
-                 anchor_lq_hw=None, anchor_native_scheme="true", use_graph=True, seed=0,
+                 anchor_lq_hw=None, anchor_native_scheme="repeat", use_graph=True, seed=0,
                  device="cuda", ring_cat=False):
         cfg = model.cfg
         if anchor not in (None, "frame", "chunk"):

@@ -215,7 +215,7 @@ def test_stream_native_anchor_repeat_scheme(refiner_model):
         return StreamingRefiner(refiner_model, H, W, ctx, chunk=CHUNK, kv_len=KV, seed=1,
                                 device=DEV, use_graph=False, anchor="frame",
                                 anchor_lq_hw=(8, 12), **kw)
-    rt, rr = make(), make(anchor_native_scheme="repeat")
+    rt, rr = make(anchor_native_scheme="true"), make()  # "repeat" is the default
     print("[case] native repeat harvest", flush=True)
     rt.harvest(lqn[:, :CHUNK], 0)
     rr.harvest(lqn[:, :CHUNK], 0)
