@@ -2,7 +2,8 @@
 
 Geometries (24 heads x 128, 8x8-token query blocks, 3x3 block neighbourhood):
   c1  3x16x16   (768 tokens)    +-1 frame, fp32 CPU plumbing case
-  c2  6x34x60   (12,240 tokens) +-1 frame, ragged edge blocks (2-row, 4-col tails)
+  c2  6x34x60   (12,240 tokens) +-1 frame, ragged edge blocks (2-row, 4-col tails),
+      Q and K rotated by the 3-D RoPE of their positions
   c3  6x45x80   (21,600 tokens) +-1 frame, ragged 5-row tail blocks
   c4  2 query frames of 45x80 against a 4-frame cache + the 2 current frames,
       the reference's streaming rule (one query run (0, 2, 0, 6))
@@ -10,7 +11,9 @@ Geometries (24 heads x 128, 8x8-token query blocks, 3x3 block neighbourhood):
       streaming KV of up to 12 frames, optional LQ anchor
 
 Inputs: ``torch.Generator("cpu").manual_seed(seed)``, fp32 draws in the order
-Q, K, V (then K_cache, V_cache for c4), each ~ N(0,1) * 128^-1/2, cast to the
+Q, K, V (then K_cache, V_cache for c4), each ~ N(0,1) * 128^-1/2; for c2, Q and
+K are then rotated by the 3-D RoPE of their (frame, row, column) positions
+(models.py:173-214, theta 10000, 44/42/42 dims, frame offset 0); cast to the
 run dtype; generated on the CPU so every consumer sees identical bits.
 """
 from __future__ import annotations
@@ -26,7 +29,7 @@ HEAD_DIM = 128
 # name: (f_cur, f_cache, h, w, bh, bw, rh, rw, rule)
 WINDOW_CONFIGS = {
     "c1": dict(f_cur=3, f_cache=0, h=16, w=16, bh=8, bw=8, rh=1, rw=1, rule="sym1"),
-    "c2": dict(f_cur=6, f_cache=0, h=34, w=60, bh=8, bw=8, rh=1, rw=1, rule="sym1"),
+    "c2": dict(f_cur=6, f_cache=0, h=34, w=60, bh=8, bw=8, rh=1, rw=1, rule="sym1", rope=True),
     "c3": dict(f_cur=6, f_cache=0, h=45, w=80, bh=8, bw=8, rh=1, rw=1, rule="sym1"),
     "c4": dict(f_cur=2, f_cache=4, h=45, w=80, bh=8, bw=8, rh=1, rw=1, rule="stream"),
     "prod": dict(f_cur=3, f_cache=9, h=45, w=80, bh=4, bw=4, rh=3, rw=3, rule="stream"),
@@ -68,6 +71,11 @@ def make_window_inputs(name: str, dtype=torch.bfloat16, device="cpu", seed=0, te
     kc = vc = None
     if s_cache:
         kc, vc = draw(s_cache), draw(s_cache)
+    if c.get("rope"):
+        from .model import SRDiTConfig, rope_apply, rope_table
+        tab = rope_table(SRDiTConfig(), c["f_cur"], c["h"], c["w"], 0, "cpu")
+        q = rope_apply(q[0], tab).unsqueeze(0)
+        k = rope_apply(k[0], tab).unsqueeze(0)
     if temperature != 1.0:
         q = q * temperature
         k = k * temperature

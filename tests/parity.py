@@ -60,3 +60,23 @@ def passes_attention(out, ref, *, rel_l2=REL_L2, row_rel=ROW_REL):
 def passes_abs_bounds_only(out, ref):
     m = metrics(out, ref)
     return m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS
+
+
+def rope_table_ref(f, h, w, head_dim=128, theta=10000.0, t_offset=0, device="cpu"):
+    """Per-token RoPE phasors [f*h*w, 1, head_dim/2] (complex128) straight from the
+    formulas of models.py:80-97 and :173-214: complex pair c of a head is
+    exp(i * pos * theta^(-2 c'/dim_axis)) with the pairs split 22/21/21 (for
+    head_dim 128) over frame (pos = t_offset + t), row and column, in that order."""
+    c = head_dim // 2
+    ch = c // 3
+    ct = c - 2 * ch
+    def axis(n, pairs, off=0):
+        pos = torch.arange(n, dtype=torch.float64) + off
+        inv = theta ** (-2.0 * torch.arange(pairs, dtype=torch.float64) / (2 * pairs))
+        ang = pos[:, None] * inv[None, :]
+        return torch.complex(torch.cos(ang), torch.sin(ang))
+    ft, fh, fw = axis(f, ct, t_offset), axis(h, ch), axis(w, ch)
+    tab = torch.cat([ft.view(f, 1, 1, ct).expand(f, h, w, ct),
+                     fh.view(1, h, 1, ch).expand(f, h, w, ch),
+                     fw.view(1, 1, w, ch).expand(f, h, w, ch)], dim=-1)
+    return tab.reshape(f * h * w, 1, c).to(device)

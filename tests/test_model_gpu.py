@@ -15,6 +15,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import blockgrid as obg
+from parity import rope_table_ref
 from sr_dit import model as mdl
 
 pytestmark = pytest.mark.gpu
@@ -41,17 +42,12 @@ def _ref_linear(lin, x):
 
 
 def _ref_rope(x, grid, cfg):
-    """rope_apply (models.py:173-214) in complex128."""
+    """rope_apply (models.py:173-214) in complex128, on a phasor table built in the
+    test from the formulas (parity.rope_table_ref), not from the product's."""
     f, h, w = grid
     s, n, d = x.shape
     c = d // 2
-    dt, dh, dw = mdl.rope_axis_dims(d)
-    ft = mdl.rope_params(cfg.rope_max_seq_len, dt, cfg.rope_theta)
-    fh = mdl.rope_params(cfg.rope_max_seq_len, dh, cfg.rope_theta)
-    fw = mdl.rope_params(cfg.rope_max_seq_len, dw, cfg.rope_theta)
-    fr = torch.cat([ft[:f].view(f, 1, 1, -1).expand(f, h, w, -1),
-                    fh[:h].view(1, h, 1, -1).expand(f, h, w, -1),
-                    fw[:w].view(1, 1, w, -1).expand(f, h, w, -1)], dim=-1).reshape(s, 1, c).to(x.device)
+    fr = rope_table_ref(f, h, w, d, cfg.rope_theta, device=x.device)
     xc = torch.view_as_complex(x.to(torch.float64).reshape(s, n, c, 2))
     return torch.view_as_real(xc * fr).flatten(2).to(x.dtype)
 
@@ -234,7 +230,7 @@ def test_fused_rmsnorm_rope():
     _lib.rmsnorm_rope(x, wt, 1e-6, cs, 128, out)
     xf = x.float()
     y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * wt
-    ref = mdl.rope_apply(y.view(s, 24, 128), tab).view(s, 3072)
+    ref = _ref_rope(y.view(s, 24, 128), (f, h, w), cfg).view(s, 3072)
     # a rotated pair can cancel: bound by the magnitude of the pair
     yp = y.float().view(s, 1536, 2).abs().sum(-1, keepdim=True).expand(s, 1536, 2).reshape(s, 3072)
     _bf16_close(out, ref, frac=2e-3, scale=yp)
