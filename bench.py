@@ -46,8 +46,10 @@ def parse():
                     help="skip the shipped-geometry (4x4 blocks, radius 3) window timings")
     ap.add_argument("--no-stream", action="store_true",
                     help="skip the streaming SR loop (chunks over the ring KV cache) measurement")
-    ap.add_argument("--step-iters", type=int, default=5,
-                    help="timed graph replays of the refiner step")
+    ap.add_argument("--step-iters", type=int, default=50,
+                    help="timed graph replays of the refiner forward (median reported)")
+    ap.add_argument("--no-rowwise", action="store_true",
+                    help="skip the refiner forward with row-wise fp8 scales")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="rough budget for the CPU baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -141,21 +143,24 @@ def cpu_baseline(config, budget_s):
                        f"{med * 1e3:.1f} ms; os.cpu_count()={os.cpu_count()}; {cpu_model}")}
 
 
-def build_model(layers=30):
-    """The 5B refiner (random weights, fp8 per-tensor Linears) and its build time."""
+def build_model(layers=30, scaling="tensor"):
+    """The 5B refiner (random weights, fp8 Linears with ``scaling`` scales) and its build time."""
     import torch
     from sr_dit import model as mdl
 
     t0 = time.perf_counter()
     model = mdl.build_refiner(mdl.SRDiTConfig(num_layers=layers), device=torch.device("cuda:0"),
-                              scaling="tensor", seed=0)
+                              scaling=scaling, seed=0)
     return model, time.perf_counter() - t0
 
 
-def refiner_step(model, build_s, steps, warmup):
-    """One SR-DiT 5B refiner step at 2K: 30 blocks + head on 21,600 tokens with 512
-    context tokens, fp8 per-tensor linears, window self-attention as in c3, dense
-    cross-attention, captured once in a HIP graph and replayed."""
+def refiner_step(model, build_s, replays, warmup):
+    """One SR-DiT 5B refiner forward at 2K, whole: time and text embeddings, patch
+    embedding of the 48x6x90x160 latent, 30 blocks (fp8 linears, window
+    self-attention as in c3, cross-attention to 512 text tokens), head and
+    unpatchify (models.py:1827-1875, :2234-2257), captured once in a HIP graph.
+    Each replay is timed on its own with HIP events on the replay stream; the
+    median and mean over ``replays`` replays are reported."""
     import torch
     from sr_dit import workloads as wl
     from sr_dit.fp8_linear import Fp8Linear
@@ -167,14 +172,12 @@ def refiner_step(model, build_s, steps, warmup):
     s_tok = f * h * w
     geom = model.geometry(f, h, w, cfg.text_len, dev)
     g = torch.Generator("cpu").manual_seed(0)
-    x = torch.randn(s_tok, cfg.dim, generator=g).to(torch.bfloat16).to(dev)
-    ctx = torch.randn(cfg.text_len, cfg.dim, generator=g).to(torch.bfloat16).to(dev)
-    e0 = (torch.randn(1, 6, cfg.dim, generator=g) / cfg.dim ** 0.5).to(dev)
-    e = (torch.randn(1, cfg.dim, generator=g) / cfg.dim ** 0.5).to(dev)
+    latent = torch.randn(cfg.in_dim, f, 2 * h, 2 * w, generator=g).to(dev)
+    ctx_raw = torch.randn(cfg.text_len, cfg.text_dim, generator=g).to(torch.bfloat16).to(dev)
+    t = torch.tensor([625.0], device=dev)
 
     def fwd():
-        y = model.blocks_forward(x, e0, ctx, geom)
-        return model.head(y, e)
+        return model.forward(latent, t, ctx_raw, geom)
 
     # useful work: every fp8 GEMM (2*M*N*K), window attention and cross-attention
     gemm = 0
@@ -185,45 +188,64 @@ def refiner_step(model, build_s, steps, warmup):
                 gemm += 2 * rows * m.in_features * m.out_features
     win = wl.plan_useful_flops(geom["plan"]) * layers
     cross = 4 * s_tok * cfg.text_len * cfg.head_dim * cfg.num_heads * layers
-    total = gemm + win + cross
+    ends = 2 * s_tok * cfg.dim * (cfg.in_dim * 4 + cfg.out_dim * 4)  # patch embedding + head
+    total = gemm + win + cross + ends
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(replays)]
     with torch.no_grad():
         for _ in range(max(1, warmup)):
-            fwd()
+            want = fwd()
         torch.cuda.synchronize()
-        e0_ev, e1_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0_ev.record()
+        ev[0][0].record(stream)
         fwd()
-        e1_ev.record()
+        ev[0][1].record(stream)
         torch.cuda.synchronize()
-        eager_ms = e0_ev.elapsed_time(e1_ev)
+        eager_ms = ev[0][0].elapsed_time(ev[0][1])
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            fwd()
+            y = fwd()
         graph.replay()
         torch.cuda.synchronize()
-        e0_ev.record()
-        for _ in range(steps):
+        same = bool(torch.equal(y, want))
+        for a, b in ev:
+            a.record(stream)
             graph.replay()
-        e1_ev.record()
+            b.record(stream)
         torch.cuda.synchronize()
-        ms = e0_ev.elapsed_time(e1_ev) / steps
-    return {"ms_per_step": round(ms, 3), "eager_ms": round(eager_ms, 3), "steps": steps,
+        times = [a.elapsed_time(b) for a, b in ev]
+    ms = statistics.median(times)
+    return {"ms_per_step": round(ms, 3), "mean_ms": round(statistics.fmean(times), 3),
+            "min_ms": round(min(times), 3), "max_ms": round(max(times), 3), "replays": replays,
+            "eager_ms": round(eager_ms, 3), "graph_equals_eager": same,
             "hip_graph": True, "layers": layers, "tokens": s_tok, "context_tokens": cfg.text_len,
-            "linears": "fp8 e4m3, per-tensor scales", "useful_tflop": round(total / 1e12, 2),
-            "gemm_tflop": round(gemm / 1e12, 2), "tflops": round(total / (ms * 1e-3) / 1e12, 1),
-            "build_s": round(build_s, 1),
-            "data": "synthetic: N(0,0.02) weights, N(0,1) activations and context"}
+            "scope": "time + text embeddings, patch embedding, 30 blocks, head, unpatchify",
+            "linears": "fp8 e4m3, " + ("per-tensor" if scaling_of(model) == "tensor"
+                                       else "row-wise (per-token activation, per-channel weight)")
+                       + " scales",
+            "useful_tflop": round(total / 1e12, 2), "gemm_tflop": round(gemm / 1e12, 2),
+            "tflops": round(total / (ms * 1e-3) / 1e12, 1), "build_s": round(build_s, 1),
+            "data": "synthetic: N(0,0.02) weights, N(0,1) latent and text context"}
 
 
-def stream_chunks(model, chunks=6, timed=2, anchor=None):
-    """The streaming SR loop at the shipped settings: 45x80-token frames (90x160
-    latent), 3-frame chunks, a 9-frame KV cache per layer kept in place (ring),
-    4x4-block radius-3 windows, the warped 4-step schedule plus the refresh pass
-    per chunk (5 forwards of the 30-layer model), every forward a HIP graph
-    replay.  ``anchor`` "frame": the shipped LQ anchor (run_inference.sh:59-65),
-    harvested per chunk by one more forward over the LQ frames.  The first
-    chunks fill the cache (one graph per cache length); the last ``timed``
-    chunks run at the full 12-frame KV and are timed."""
+def scaling_of(model):
+    from sr_dit.fp8_linear import Fp8Linear
+    for m in model.modules():
+        if isinstance(m, Fp8Linear):
+            return m.scaling
+    return "none"
+
+
+def stream_chunks(model, chunks=6, timed=2, anchor=None, sigma_start=0.6251):
+    """The streaming SR loop: 45x80-token frames (90x160 latent), 3-frame chunks, a
+    9-frame KV cache per layer kept in place (ring), 4x4-block radius-3 windows,
+    every forward a HIP graph replay.  ``sigma_start`` 0.6251 is the shipped
+    schedule (sr_dit_5b.yaml:65): of the warped list 1000/937.5/833.3/625 only
+    t=625 remains, so a chunk is one denoising forward plus the refresh pass;
+    1.0 keeps all four steps.  ``anchor`` "frame": the LQ anchor
+    (run_inference.sh:59-65), harvested per chunk by one more forward over the LQ
+    frames.  The first chunks fill the cache (one graph per cache length); the
+    last ``timed`` chunks run at the full 12-frame KV and are timed."""
     import torch
     from sr_dit.stream import StreamingRefiner
 
@@ -235,15 +257,17 @@ def stream_chunks(model, chunks=6, timed=2, anchor=None):
     ctx = torch.randn(cfg.text_len, cfg.text_dim, generator=g).to(torch.bfloat16).to(dev)
     lq = torch.randn(cfg.in_dim, chunk * chunks, 2 * h, 2 * w, generator=g).to(dev)
     t0 = time.perf_counter()
-    r = StreamingRefiner(model, h, w, ctx, chunk=chunk, kv_len=9, device=dev, anchor=anchor)
+    r = StreamingRefiner(model, h, w, ctx, chunk=chunk, kv_len=9, device=dev, anchor=anchor,
+                         sigma_start=sigma_start)
     per_chunk = []
+    stream = torch.cuda.current_stream(dev)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     for c in range(chunks):
         sl = slice(c * chunk, (c + 1) * chunk)
-        e0.record()
+        e0.record(stream)
         r.refine_chunk(noise[:, sl], c * chunk, lq[:, sl] if anchor else None)
-        e1.record()
+        e1.record(stream)
         torch.cuda.synchronize()
         per_chunk.append(e0.elapsed_time(e1))
     wall = time.perf_counter() - t0
@@ -251,20 +275,23 @@ def stream_chunks(model, chunks=6, timed=2, anchor=None):
     ms = sum(steady) / len(steady)
     # one eager forward at the full cache for comparison
     r.use_graph = False
-    e0.record()
+    e0.record(stream)
     r.forward(noise[:, :chunk], r.steps[0], chunks * chunk, anchored=anchor is not None)
-    e1.record()
+    e1.record(stream)
     torch.cuda.synchronize()
     eager_fwd = e0.elapsed_time(e1)
     n_fwd = len(r.steps) + 1 + (1 if anchor else 0)
+    sched = ("shipped one-step schedule (sigma_start 0.6251: t=625)" if len(r.steps) == 1
+             else f"{len(r.steps)}-step schedule (sigma_start {sigma_start})")
     return {"workload": "streaming SR loop, 5B refiner (30 layers), 3 x 45x80-token chunk vs "
-                        "9 cached frames (ring), 4x4 blocks radius 3, 4 denoising steps + "
-                        "KV refresh per chunk, 512 context tokens"
+                        "9 cached frames (ring), 4x4 blocks radius 3, " + sched
+                        + " + KV refresh per chunk, 512 context tokens"
                         + (f", LQ anchor ({anchor}-aligned, harvested per chunk)" if anchor
                            else ", no LQ anchor"),
             "ms_per_chunk": round(ms, 2), "ms_per_forward": round(ms / n_fwd, 2),
             "eager_ms_per_forward": round(eager_fwd, 2), "forwards_per_chunk": n_fwd,
-            "steps": [round(t, 2) for t in r.steps], "kv_frames": 9 + chunk,
+            "sigma_start": sigma_start, "steps": [round(t, 2) for t in r.steps],
+            "kv_frames": 9 + chunk,
             "chunk_ms_all": [round(x, 1) for x in per_chunk], "hip_graphs": len(r._graphs),
             "wall_s": round(wall, 1),
             "data": "synthetic: N(0,0.02) weights, N(0,1) noise latents and context"}
@@ -408,7 +435,15 @@ def main():
         if not args.no_stream:
             result["stream"] = stream_chunks(model)
             result["stream_lq_anchor"] = stream_chunks(model, anchor="frame")
+            result["stream_4step"] = stream_chunks(model, sigma_start=1.0)
         del model
+        torch.cuda.empty_cache()
+        if not (args.no_step or args.no_rowwise):
+            model, build_s = build_model(scaling="rowwise")
+            result["refiner_step_rowwise"] = refiner_step(model, build_s,
+                                                          max(10, args.step_iters // 5), 1)
+            del model
+            torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     print(json.dumps(result), flush=True)
