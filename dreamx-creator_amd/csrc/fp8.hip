@@ -27,6 +27,7 @@
 #include "common.h"
 #include "fp8_common.h"
 
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -635,4 +636,83 @@ extern "C" int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, 
                                                        static_cast<uint8_t*>(xq), scale, amax_ws);
   SRDIT_LAUNCH_CHECK("quant_tensor_kernel");
   return SRDIT_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The per-tensor fp8 Linear as one call that allocates nothing.
+//
+// `scratch` holds what srdit_fp8_quant_tensor + srdit_fp8_gemm_ex keep in
+// caller-provided buffers: the amax word (bytes 0-3), the activation scale
+// (bytes 4-7) and, from byte 256, the e4m3 codes of the activation (at most
+// SRDIT_LINEAR_SCRATCH_CODES bytes, so M*K is limited to that).  Each device
+// holds its own copy of the array from the library's first use on it until
+// the process ends.  Host code never passes the array's name to a kernel: it
+// is a host-side stand-in for the symbol.  The device address comes from
+// hipGetSymbolAddress, taken once per device on the first call with that
+// device current.  Every call on one device shares that device's array:
+// calls that overlap on one device (two streams, or two host threads) race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[256 + SRDIT_LINEAR_SCRATCH_CODES];
+
+namespace srdit {
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxScratchDevices] = {};
+
+int scratch_of_current_device(void** out, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  SRDIT_REQUIRE(e == hipSuccess, "%s: hipGetDevice failed: %s", who, hipGetErrorString(e));
+  SRDIT_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "%s: device %d out of range", who, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+                hipGetErrorString(e));
+      return SRDIT_EHIP;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return SRDIT_OK;
+}
+}  // namespace
+}  // namespace srdit
+
+extern "C" int srdit_fp8_linear_tensor_static(const void* x, int64_t M, int64_t K, int64_t ldx,
+                                              int dtype, const void* w, const float* w_scale,
+                                              int64_t w_scale_cols, const void* bias, void* out,
+                                              int64_t N, int64_t ldo, void* stream) {
+  const char* who = "srdit_fp8_linear_tensor_static";
+  SRDIT_REQUIRE(M > 0 && K > 0 && M * K <= SRDIT_LINEAR_SCRATCH_CODES,
+                "%s: M*K = %lld exceeds the static scratch (%lld e4m3 codes); use "
+                "srdit_fp8_quant_tensor + srdit_fp8_gemm_ex with caller buffers", who,
+                (long long)(M * K), (long long)SRDIT_LINEAR_SCRATCH_CODES);
+  void* base = nullptr;
+  if (int rc = scratch_of_current_device(&base, who)) return rc;
+  uint8_t* sb = static_cast<uint8_t*>(base);
+  uint32_t* amax = reinterpret_cast<uint32_t*>(sb);
+  float* scale = reinterpret_cast<float*>(sb + 4);
+  uint8_t* codes = sb + 256;
+  if (int rc = check_quant_args(who, x, M, K, ldx, codes, scale)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = dispatch_quant_dtype(dtype, [&](auto tag) -> int {
+    using T = std::remove_const_t<std::remove_pointer_t<decltype(tag)>>;
+    const int64_t rows4 = (M + 3) / 4;
+    const unsigned blocks = (unsigned)(rows4 < 4096 ? rows4 : 4096);
+    clear_u32_kernel<<<1, 1, 0, s>>>(amax);
+    SRDIT_LAUNCH_CHECK("clear_u32_kernel");
+    amax_kernel<T><<<blocks, 256, 0, s>>>(static_cast<const T*>(x), M, K, ldx, amax);
+    SRDIT_LAUNCH_CHECK("amax_kernel");
+    quant_tensor_kernel<T><<<blocks, 256, 0, s>>>(static_cast<const T*>(x), M, K, ldx, codes,
+                                                  scale, amax);
+    SRDIT_LAUNCH_CHECK("quant_tensor_kernel");
+    return SRDIT_OK;
+  });
+  if (rc) return rc;
+  return fp8_gemm_launch(codes, w, scale, 1, w_scale, w_scale_cols, bias, out, M, N, K, ldo,
+                         SRDIT_GEMM_MFMA, nullptr, stream, who);
 }

@@ -60,6 +60,8 @@ SIGNATURES = {
     "srdit_last_error": (_c_int, [ctypes.c_char_p, _c_int]),
     "srdit_version": (_c_int, []),
     "srdit_copy_bytes": (_c_int, [_c_p, _c_p, _c_i64, _c_p]),
+    "srdit_fp8_linear_tensor_static": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p,
+                                                _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_p]),
 }
 
 _LIB = None
@@ -244,6 +246,37 @@ def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None, force_mfm
                                   int(epilogue) | (GEMM_MFMA if force_mfma else 0),
                                   _ptr(amax_out), _stream(a.device))
     _check(rc, "srdit_fp8_gemm_ex")
+
+
+#: capacity of the static scratch of srdit_fp8_linear_tensor_static (activation codes)
+LINEAR_SCRATCH_CODES = 64 << 20
+
+
+def fp8_linear_tensor_static(x, w, w_scale, bias, out):
+    """The per-tensor fp8 Linear with no caller workspace and no allocation:
+    out [M, N] bf16 = quantise(x [M, K]) . w [N, K]^T * scales + bias, the
+    activation's amax, scale and codes in the library's static per-device scratch
+    (M*K <= LINEAR_SCRATCH_CODES).  Calls that overlap on one device race."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.dtype not in (torch.bfloat16, torch.float16,
+                                                            torch.float32):
+        raise ValueError("fp8_linear_tensor_static: x must be 2-D bf16/fp16/fp32 with unit "
+                         "column stride")
+    if w.dtype != torch.float8_e4m3fn or w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("fp8_linear_tensor_static: w must be a contiguous 2-D float8_e4m3fn tensor")
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"fp8_linear_tensor_static: inner dims differ ({K} vs {w.shape[1]})")
+    if w_scale.dtype != torch.float32 or not w_scale.is_contiguous():
+        raise ValueError("fp8_linear_tensor_static: w_scale must be contiguous float32")
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError(f"fp8_linear_tensor_static: out must be bf16 [{M}, {N}] with unit "
+                         "column stride")
+    dt = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}[x.dtype]
+    rc = load().srdit_fp8_linear_tensor_static(_ptr(x), M, K, x.stride(0), dt, _ptr(w),
+                                               _ptr(w_scale), int(w_scale.numel()), _ptr(bias),
+                                               _ptr(out), N, out.stride(0), _stream(x.device))
+    _check(rc, "srdit_fp8_linear_tensor_static")
 
 
 def fp8_quant_tensor_gelu(x, xq, scale, amax_ws, h=None):

@@ -290,6 +290,30 @@ int srdit_version(void);
  */
 int srdit_copy_bytes(const void* src, void* dst, int64_t bytes, void* stream);
 
+/* Capacity of the static scratch of srdit_fp8_linear_tensor_static, in e4m3
+ * codes of the activation: M*K may not exceed it (64 MiB). */
+#define SRDIT_LINEAR_SCRATCH_CODES ((int64_t)64 << 20)
+
+/*
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The per-tensor fp8 Linear in one call that allocates nothing:
+ *   out = srdit_fp8_gemm_ex(e4m3(x / s_x), w, s_x, w_scale, bias) with
+ *   s_x = max(amax(|x|) * fl32(1/448), 1e-12),
+ * the same kernels and results as srdit_fp8_quant_tensor followed by
+ * srdit_fp8_gemm_ex(..., SRDIT_GEMM_MFMA, NULL), with the amax word, the
+ * scale and the activation codes in a static per-device scratch array
+ * instead of caller buffers.  Rejects M*K > SRDIT_LINEAR_SCRATCH_CODES
+ * (SRDIT_EINVAL).  x [M, K] bf16/fp16/fp32 (dtype, row stride ldx); w [N, K]
+ * e4m3; w_scale [1] or [N] (w_scale_cols 1 or N); bias bf16 [N] or NULL;
+ * out bf16 [M, N] (row stride ldo).  Calls that overlap on one device race
+ * on the shared scratch; each device holds its array until the process ends.
+ */
+int srdit_fp8_linear_tensor_static(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype,
+                                   const void* w, const float* w_scale, int64_t w_scale_cols,
+                                   const void* bias, void* out, int64_t N, int64_t ldo,
+                                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif
