@@ -126,10 +126,17 @@ __global__ __launch_bounds__(256) void amax_kernel(const T* __restrict__ x, int6
   uint32_t amax = 0;
   for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
     const T* xr = x + row * ldx;
-    for (int64_t c = lane; c < nchunk; c += 64) {
-      float f[8];
-      Load8<T>::get(xr, c, f);
-      amax = abs_bits_max8(f, amax);
+    // four chunks per lane in flight; a clamped index re-reads a chunk already
+    // counted, which leaves the max unchanged
+    for (int64_t c0 = lane; c0 < nchunk; c0 += 256) {
+      float f[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t c = c0 + 64 * u;
+        Load8<T>::get(xr, c < nchunk ? c : nchunk - 1, f[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) amax = abs_bits_max8(f[u], amax);
     }
   }
   amax = wave_umax(amax);
@@ -140,6 +147,8 @@ __global__ __launch_bounds__(256) void amax_kernel(const T* __restrict__ x, int6
     atomicMax(amax_ws, m);
   }
 }
+
+constexpr int QU = 4;  // 16-byte chunks per lane in flight in the quantise pass
 
 template <typename T>
 __global__ __launch_bounds__(256) void quant_tensor_kernel(const T* __restrict__ x, int64_t M,
@@ -155,10 +164,20 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const T* __restrict__
   for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
     const T* xr = x + row * ldx;
     uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
-    for (int64_t c = lane; c < nchunk; c += 64) {
-      float f[8];
-      Load8<T>::get(xr, c, f);
-      qr[c] = to_e4m3x8(f, sd);
+    // QU chunks per lane in flight: the loads (indices clamped into the row, so
+    // they need no branch) all issue before the first conversion.
+    for (int64_t c0 = lane; c0 < nchunk; c0 += 64 * QU) {
+      float f[QU][8];
+#pragma unroll
+      for (int u = 0; u < QU; ++u) {
+        const int64_t c = c0 + 64 * u;
+        Load8<T>::get(xr, c < nchunk ? c : nchunk - 1, f[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < QU; ++u) {
+        const int64_t c = c0 + 64 * u;
+        if (c < nchunk) qr[c] = to_e4m3x8(f[u], sd);
+      }
     }
   }
 }
