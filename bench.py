@@ -351,6 +351,18 @@ def production_window(steps, warmup=3):
     return res
 
 
+def leg(name, fn, *a, **kw):
+    """Run one measurement leg inside a named range (a roctx range under rocprofv3
+    --marker-trace), so kernel traces can be split by leg."""
+    import torch
+    torch.cuda.nvtx.range_push(name)
+    try:
+        return fn(*a, **kw)
+    finally:
+        torch.cuda.synchronize()
+        torch.cuda.nvtx.range_pop()
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -381,6 +393,7 @@ def main():
         bgh.run_blockgrid_hip(q, k, v, out, plan=plan, f_cur=spec.f_cur, h=spec.h, w=spec.w,
                               n=n, d=d)
 
+    torch.cuda.nvtx.range_push("window_" + cfg)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -394,6 +407,7 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    torch.cuda.nvtx.range_pop()
     ms = e0.elapsed_time(e1) / args.steps
 
     flops = wl.plan_useful_flops(plan)
@@ -427,21 +441,23 @@ def main():
         "wall_s_timed_region": round(wall, 4),
     }
     if not args.no_prod:
-        result["production_window"] = production_window(20)
+        result["production_window"] = leg("production_window", production_window, 20)
     if not (args.no_step and args.no_stream):
         model, build_s = build_model()
         if not args.no_step:
-            result["refiner_step"] = refiner_step(model, build_s, args.step_iters, 1)
+            result["refiner_step"] = leg("refiner_step", refiner_step, model, build_s,
+                                        args.step_iters, 1)
         if not args.no_stream:
-            result["stream"] = stream_chunks(model)
-            result["stream_lq_anchor"] = stream_chunks(model, anchor="frame")
-            result["stream_4step"] = stream_chunks(model, sigma_start=1.0)
+            result["stream"] = leg("stream", stream_chunks, model)
+            result["stream_lq_anchor"] = leg("stream_lq_anchor", stream_chunks, model,
+                                             anchor="frame")
+            result["stream_4step"] = leg("stream_4step", stream_chunks, model, sigma_start=1.0)
         del model
         torch.cuda.empty_cache()
         if not (args.no_step or args.no_rowwise):
             model, build_s = build_model(scaling="rowwise")
-            result["refiner_step_rowwise"] = refiner_step(model, build_s,
-                                                          max(10, args.step_iters // 5), 1)
+            result["refiner_step_rowwise"] = leg("refiner_step_rowwise", refiner_step, model,
+                                                 build_s, max(10, args.step_iters // 5), 1)
             del model
             torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
