@@ -243,35 +243,53 @@ void window_group_kernel(GroupArgs a) {
   f32x16_t oacc[DT];
   const int m = m0 + 32 * qhalf + c;
   const bool qvalid = has_member && m < lq;
-  int64_t qflat;
+  // Token of row r (0..31) of this wavefront's 32 queries, clamped into Q;
+  // row_ok: the row is one of the window's queries.
+  auto row_token = [&](int r) __attribute__((always_inline)) -> int {
+    const int mr = m0 + 32 * qhalf + r;
+    const int mm = (has_member && mr < lq) ? mr : 0;
+    const int qs = q_sp > 0 ? q_sp : 1, qw = qw_l > 0 ? qw_l : 1;
+    const int fr = fdiv(mm, qs, 1.0f / static_cast<float>(qs));
+    const int rr = mm - fr * q_sp;
+    const int hh = fdiv(rr, qw, 1.0f / static_cast<float>(qw));
+    const int ww = rr - hh * qw_l;
+    const int t = (q_t0 + fr) * L + (q_h0 + hh) * a.W + (q_w0 + ww);
+    return t < 0 ? 0 : (t >= a.q_tokens ? static_cast<int>(a.q_tokens) - 1 : t);
+  };
+  auto row_ok = [&](int r) __attribute__((always_inline)) -> bool {
+    return has_member && m0 + 32 * qhalf + r < lq;
+  };
   int qframe;  // this lane's query frame within the window
+  // The anchored forms (AMODE 1, 2) sit at the register limit: they load Q
+  // straight into registers and store O from them, each lane its own query's
+  // row.  The plain form stages both through LDS (the prologue and epilogue).
+  int64_t qflat = 0;
   {
     const int mm = qvalid ? m : 0;
     const int qs = q_sp > 0 ? q_sp : 1, qw = qw_l > 0 ? qw_l : 1;
     const int fr = fdiv(mm, qs, 1.0f / static_cast<float>(qs));
     qframe = fr;
-    const int r = mm - fr * q_sp;
-    const int hh = fdiv(r, qw, 1.0f / static_cast<float>(qw));
-    const int ww = r - hh * qw_l;
-    qflat = static_cast<int64_t>(q_t0 + fr) * L + static_cast<int64_t>(q_h0 + hh) * a.W +
-            (q_w0 + ww);
-    qflat = qflat < 0 ? 0 : (qflat >= a.q_tokens ? a.q_tokens - 1 : qflat);
-    const V8* qp = reinterpret_cast<const V8*>(reinterpret_cast<const T*>(a.q) + head * D +
-                                               qflat * tok + hf * (D / 2));
-    // Q enters the S^T MFMA pre-scaled by scale*log2(e) (rounded once to T),
-    // so the scores come out in log2 units.
-    // Every lane loads (qflat is clamped in bounds), so the loads issue back to
-    // back with no exec branches between them; lanes past the window's queries
-    // are zeroed after the load.
-    V8 raw[KS];
+    if constexpr (AMODE != 0) {
+      const int r = mm - fr * q_sp;
+      const int hh = fdiv(r, qw, 1.0f / static_cast<float>(qw));
+      const int ww = r - hh * qw_l;
+      qflat = static_cast<int64_t>(q_t0 + fr) * L + static_cast<int64_t>(q_h0 + hh) * a.W +
+              (q_w0 + ww);
+      qflat = qflat < 0 ? 0 : (qflat >= a.q_tokens ? a.q_tokens - 1 : qflat);
+      const V8* qp = reinterpret_cast<const V8*>(reinterpret_cast<const T*>(a.q) + head * D +
+                                                 qflat * tok + hf * (D / 2));
+      // Q enters the S^T MFMA pre-scaled by scale*log2(e) (rounded once to T), so
+      // the scores come out in log2 units; lanes past the window's queries hold 0.
+      V8 raw[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) raw[ks] = qp[ks];
+      for (int ks = 0; ks < KS; ++ks) raw[ks] = qp[ks];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      float x[8];
+      for (int ks = 0; ks < KS; ++ks) {
+        float x[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = qvalid ? static_cast<float>(raw[ks][i]) * a.scale_log2 : 0.f;
-      qf[ks] = E::pack8(x);
+        for (int i = 0; i < 8; ++i) x[i] = qvalid ? static_cast<float>(raw[ks][i]) * a.scale_log2 : 0.f;
+        qf[ks] = E::pack8(x);
+      }
     }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16_t{};
@@ -495,12 +513,50 @@ void window_group_kernel(GroupArgs a) {
     return ((wact >> (fs_ & 31)) & 1u) != 0 && fs_ < 32;
   };
 
-  // Prologue: K and V of steps 0 and 1; S^T of step 0.
-  if (nsteps > 0) {
-    fill_next(0);
-    if (nsteps > 1) fill_next(1);
+  // Prologue.  Each wavefront stages its 32 query rows into its own 8 KB of the
+  // V ring's stages 1 and 2 with the fill DMA: whole 256-byte rows per 16 lanes
+  // in the K tile layout (row r, chunk L at slot L ^ swz_k(r)), so the loads are
+  // full cache lines and the reads below are the K operand's conflict-free
+  // pattern.  K of steps 0 and 1 and V of step 0 land with it; V of step 1
+  // follows once every wavefront has read its Q.  Then the S^T of step 0.
+  constexpr int CPKQ = D / 8, LPKQ = CPKQ, KPIQ = 64 / CPKQ;
+  const uint32_t qreg = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(vsh)) +
+                        static_cast<uint32_t>((MEMBERS + wave) * BLKB);
+  if constexpr (AMODE == 0) {
+    const uint64_t qa = reinterpret_cast<uint64_t>(reinterpret_cast<const T*>(a.q) + head * D);
+    const i32x4_t qrsrc = {static_cast<int>(static_cast<uint32_t>(qa)),
+                           static_cast<int>(static_cast<uint32_t>(qa >> 32) |
+                                            (static_cast<uint32_t>(tok_bytes) << 16)),
+                           static_cast<int>(a.q_tokens), 0x00020000};
+    const int pos = lane % CPKQ, sub_q = (lane & 15) / LPKQ;
+    static_for<NL>([&](auto qc) __attribute__((always_inline)) {
+      constexpr int qi = decltype(qc)::value;
+      const int r = qi * KPIQ + (lane >> 4) * (16 / LPKQ) + sub_q;
+      dma_x4(qrsrc, qreg + qi * 1024, row_token(r), (pos ^ swz_k<D>(r)) * 16);
+    });
   }
+  if (nsteps > 0) fill_next(0);
+  if (nsteps > 1 && (AMODE != 0 || kv_role == 0)) fill_next(1);
   fill_barrier();
+  if constexpr (AMODE == 0) {
+    // Q enters the S^T MFMA pre-scaled by scale*log2(e) (rounded once to T), so
+    // the scores come out in log2 units; lanes past the window's queries hold 0.
+    const char* qb = reinterpret_cast<const char*>(vsh) + (MEMBERS + wave) * BLKB;
+    V8 raw[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) raw[ks] = *reinterpret_cast<const V8*>(qb + lo.k[ks]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = qvalid ? static_cast<float>(raw[ks][i]) * a.scale_log2 : 0.f;
+      qf[ks] = E::pack8(x);
+    }
+  }
+  if constexpr (AMODE == 0) {
+    fill_barrier();  // every wavefront has its Q: V stage 1 is free
+    if (nsteps > 1 && kv_role == 1) fill_next(1);
+  }
   f32x16_t s_cur = f32x16_t{};
   if (nsteps > 0 && wactive(0)) s_cur = s_mfma(read_k(std::integral_constant<int, 0>{}));
 
@@ -614,24 +670,61 @@ void window_group_kernel(GroupArgs a) {
   if (j + 3 < nsteps) iteration(j + 3, I1{}, I0{});
   if (j + 4 < nsteps) iteration(j + 4, I0{}, I1{});
 
-  // O = acc / l ; lane (c, hf) writes dims dt*32 + 8*g4 + 4*hf + [0, 4) of its query
+  // O = acc / l, staged through this wavefront's 8 KB of the V ring in the Q
+  // layout (lane (c, hf) holds dims dt*32 + 8*g4 + 4*hf + [0, 4) of query c),
+  // then written out as whole 256-byte rows, 16 lanes per row.
   const float lt = half_sum(lrun);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
   uint32_t am = 0;
-  if (qvalid) {
-    T* op = reinterpret_cast<T*>(a.o) + head * D + qflat * tok;
+  if constexpr (AMODE != 0) {
+    if (qvalid) {
+      T* op = reinterpret_cast<T*>(a.o) + head * D + qflat * tok;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const f32x2_t lo2 = {oacc[dt][g4 * 4 + 0] * inv, oacc[dt][g4 * 4 + 1] * inv};
-        const f32x2_t hi2 = {oacc[dt][g4 * 4 + 2] * inv, oacc[dt][g4 * 4 + 3] * inv};
-        const auto l = __builtin_convertvector(lo2, typename E::h2);
-        const auto u = __builtin_convertvector(hi2, typename E::h2);
-        const i32x2_t w = {__builtin_bit_cast(int, l), __builtin_bit_cast(int, u)};
-        *reinterpret_cast<i32x2_t*>(op + dt * 32 + g4 * 8 + hf * 4) = w;
-        if (a.amax_out) am = max(am, max(abs_bits2(l), abs_bits2(u)));
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const f32x2_t lo2 = {oacc[dt][g4 * 4 + 0] * inv, oacc[dt][g4 * 4 + 1] * inv};
+          const f32x2_t hi2 = {oacc[dt][g4 * 4 + 2] * inv, oacc[dt][g4 * 4 + 3] * inv};
+          const auto l = __builtin_convertvector(lo2, typename E::h2);
+          const auto u = __builtin_convertvector(hi2, typename E::h2);
+          const i32x2_t w = {__builtin_bit_cast(int, l), __builtin_bit_cast(int, u)};
+          *reinterpret_cast<i32x2_t*>(op + dt * 32 + g4 * 8 + hf * 4) = w;
+          if (a.amax_out) am = max(am, max(abs_bits2(l), abs_bits2(u)));
+        }
+    }
+    if (a.amax_out) wave_amax_out(a.amax_out, am);
+    return;
+  }
+  fill_barrier();  // every wavefront is done with the ring
+  char* ob = reinterpret_cast<char*>(vsh) + (MEMBERS + wave) * BLKB;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x2_t lo2 = {oacc[dt][g4 * 4 + 0] * inv, oacc[dt][g4 * 4 + 1] * inv};
+      const f32x2_t hi2 = {oacc[dt][g4 * 4 + 2] * inv, oacc[dt][g4 * 4 + 3] * inv};
+      const auto l = __builtin_convertvector(lo2, typename E::h2);
+      const auto u = __builtin_convertvector(hi2, typename E::h2);
+      const i32x2_t w = {__builtin_bit_cast(int, l), __builtin_bit_cast(int, u)};
+      const int chunk = dt * 4 + g4;
+      *reinterpret_cast<i32x2_t*>(ob + (c * CPKQ + (chunk ^ swz_k<D>(c))) * 16 + hf * 8) = w;
+      if (a.amax_out && qvalid) am = max(am, max(abs_bits2(l), abs_bits2(u)));
+    }
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's LDS writes done
+  compiler_fence();
+  {
+    const int pos = lane % CPKQ, sub_q = (lane & 15) / LPKQ;
+#pragma unroll
+    for (int qi = 0; qi < NL; ++qi) {
+      const int r = qi * KPIQ + (lane >> 4) * (16 / LPKQ) + sub_q;
+      const i32x4_t v = *reinterpret_cast<const i32x4_t*>(ob + (r * CPKQ + (pos ^ swz_k<D>(r))) * 16);
+      if (row_ok(r)) {
+        T* op = reinterpret_cast<T*>(a.o) + head * D + static_cast<int64_t>(row_token(r)) * tok +
+                pos * 8;
+        *reinterpret_cast<i32x4_t*>(op) = v;
       }
+    }
   }
   if (a.amax_out) wave_amax_out(a.amax_out, am);
 }
