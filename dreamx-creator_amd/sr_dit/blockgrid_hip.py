@@ -160,12 +160,12 @@ def mean_kv_tokens(plan) -> float:
     return float(lkv.double().mean())
 
 
-#: Two members per workgroup pay off only when their shared walk is long: with
-#: fewer KV tokens per window the per-workgroup Q load and O store dominate and
-#: four one-member workgroups per CU hide them better (dense attention over 512
-#: and 1024 context tokens: 193 vs 202 us and 315 vs 318 us; 2048: 556 vs 539 us;
-#: inside the full refiner step the two forms tie).
-GROUPED_MIN_KV = 1536
+#: Smallest mean KV length per window for which ``auto`` pairs members.  Since
+#: the plain kernel stages Q and O through LDS, pairs of identical-KV members
+#: win at every length measured: dense attention of 21,600 queries over 64 to
+#: 1024 context tokens, 78 vs 82 us up to 280 vs 315 us (one process, identical
+#: outputs), so no minimum applies.
+GROUPED_MIN_KV = 0
 
 
 #: ``kernel="auto"`` leaves the shared-fetch kernel off: in interleaved A/B runs
@@ -380,15 +380,15 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     ``kernel``: ``"auto"`` runs plain plans without an anchor prefix on the
     grouped kernel: with two members per workgroup sharing their K/V fetches
     (``"grouped"``) when the pairs share nearly all their KV frames (the two
-    m-tiles of one window) and the windows average at least
-    ``GROUPED_MIN_KV`` KV tokens, else with one member per workgroup (``"solo"``).
+    m-tiles of one window, or the query tiles of dense attention) and the
+    windows average at least ``GROUPED_MIN_KV`` KV tokens, else with one
+    member per workgroup (``"solo"``).
     Anchored plans run solo too (the anchor frames walked after the HR
     frames); plans beyond its limits (more than 16 HR frames per window, more
     than 32 frame slots) go to the single-window kernel (``"single"``).
     Measured on one MI355X: c2 and c3 (neighbouring-frame pairs sharing 2 of
-    3 frames), the 48-query shipped windows and dense attention over 512
-    context tokens run fastest solo, c4 (m-tile pairs, 2733 KV tokens on
-    average) grouped.  Any of the three can be forced (a forced grouped launch
+    3 frames) and the 48-query shipped windows run fastest solo; c4 (m-tile
+    pairs) and dense attention over the text context grouped.  Any of the three can be forced (a forced grouped launch
     of an anchored plan raises, as does a forced solo launch of a plan beyond
     its limits).
 
