@@ -316,9 +316,11 @@ def test_gemm_gelu_epilogue_and_amax():
     assert torch.equal(out, plain)
 
 
-def test_fused_block_matches_unfused():
+@pytest.mark.parametrize("scaling", ["tensor", "rowwise"])
+def test_fused_block_matches_unfused(scaling):
+    print(f"[case] fused vs op-by-op blocks, scaling={scaling}", flush=True)
     cfg = SMALL
-    model = mdl.build_refiner(cfg, device=DEV, scaling="tensor", seed=4)
+    model = mdl.build_refiner(cfg, device=DEV, scaling=scaling, seed=4)
     f, h, w = 3, 16, 16
     geom = model.geometry(f, h, w, cfg.text_len, DEV)
     g = torch.Generator("cpu").manual_seed(1)
