@@ -235,3 +235,28 @@ def test_stream_native_anchor_repeat_scheme(refiner_model):
         assert torch.equal(x, y), f"chunk {c}"
     for c, (x, y) in enumerate(zip(gg, a)):
         assert torch.equal(x, y), f"chunk {c}"
+
+
+def test_stream_rowwise_linears():
+    """Row-wise fp8 Linears (the reference's default scaling) in the streaming loop:
+    the fused block runs with the ring; ring in place equals the concatenation and
+    graph replays equal eager forwards, bit for bit, over 4 chunks (ring wrapped)."""
+    cfg = mdl.SRDiTConfig(num_layers=2)
+    model = mdl.build_refiner(cfg, device=DEV, scaling="rowwise", seed=0)
+    assert all(b.fusable() for b in model.blocks)
+    noise, ctx, _ = _inputs(cfg, 4)
+    ra, a = _stream(model, noise, ctx, use_graph=False)
+    rb, b = _stream(model, noise, ctx, use_graph=False, ring_cat=True)
+    rg, g = _stream(model, noise, ctx, use_graph=True)
+    assert any(hd != 0 for hd in ra.heads_seen)
+    for c, (x, y, z) in enumerate(zip(a, b, g)):
+        assert torch.isfinite(x).all()
+        assert torch.equal(x, y), f"chunk {c}"
+        assert torch.equal(x, z), f"chunk {c}"
+    # row-wise and per-tensor scales give different (both finite) results
+    _, t = _stream(refiner_model_tensor(), noise, ctx, use_graph=False)
+    assert not torch.equal(a[0], t[0])
+
+
+def refiner_model_tensor():
+    return mdl.build_refiner(mdl.SRDiTConfig(num_layers=2), device=DEV, scaling="tensor", seed=0)
