@@ -151,8 +151,9 @@ int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, const void* v
  *             k_slot | v_slot << 8), words 8-11 per member k_slot | v_slot << 5
  *             | valid rows << 10 | valid columns << 13 (0: idle; a member's
  *             active steps come first), word 12 the number of fill units.
- *             K slots < 2*members, V slots < 3*members; a fill of step s
- *             must not target a slot read at step s-1 (K) or s-2 (V) or later.
+ *             Slots index one LDS pool of 5*members 8 KB tiles shared by K
+ *             and V (indices are clamped into it); a fill issued at step s
+ *             must not target a slot read at step s or later.
  * The schedule decides which keys each member attends: a malformed one gives
  * wrong numbers; every token index is clamped into the K/V tensors.
  * ring_frames, ring_cached, ring_head, amax_out as srdit_window_attn_fwd_ex.
