@@ -11,6 +11,7 @@ the host CPU over a bounded sample, as a baseline only.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -54,6 +55,8 @@ def parse():
                     help="rough budget for the CPU baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run the library's 16-byte copy kernel over BYTES (counter calibration)")
+    ap.add_argument("--source-hash", action="store_true",
+                    help="only print the hash of the sources that decide the window kernel's traffic")
     return ap.parse_args()
 
 
@@ -70,13 +73,47 @@ def copy_calibration(nbytes, reps=5):
     print(json.dumps({"copy_calibration_bytes": nbytes, "launches": reps}), flush=True)
 
 
+# The files that decide the window kernel's memory traffic on a workload: its
+# source, the launcher's tables and launch order, the workload shapes and the
+# compiler flags.
+TRAFFIC_SOURCES = ("dreamx-creator_amd/csrc/window_group.hip",
+                   "dreamx-creator_amd/csrc/window_common.h",
+                   "dreamx-creator_amd/csrc/common.h",
+                   "dreamx-creator_amd/sr_dit/blockgrid_hip.py",
+                   "dreamx-creator_amd/sr_dit/workloads.py",
+                   "dreamx-creator_amd/sr_dit/build.py")
+
+
+def traffic_source_hash():
+    """sha256 (16 hex digits) over the traffic-deciding sources, names included."""
+    h = hashlib.sha256()
+    for rel in TRAFFIC_SOURCES:
+        h.update(rel.encode())
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def profile_traffic(config):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
-    path = os.path.join(ROOT, "profiles", f"window_attn_{config}_pmc.md")
+    """(HBM bytes per launch, where from) out of the committed rocprofv3 PMC summary.
+
+    The summary records the source hash of the build it measured; a summary of
+    other sources is stale and gives no figure (None), so a kernel change never
+    reports the old kernel's traffic."""
+    rel = f"profiles/window_attn_{config}_pmc.md"
+    path = os.path.join(ROOT, rel)
     if not os.path.exists(path):
-        return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
-    return float(m.group(1)) if m else None
+        return None, f"no PMC summary {rel}"
+    text = open(path).read()
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    hm = re.search(r"source_hash:\s*([0-9a-f]+)", text)
+    cur = traffic_source_hash()
+    if not m:
+        return None, f"{rel} holds no traffic figure"
+    if not hm or hm.group(1) != cur:
+        return None, (f"stale: {rel} measured sources {hm.group(1) if hm else '(unstamped)'}, "
+                      f"this build's are {cur}")
+    return float(m.group(1)), f"{rel} (FETCH_SIZE + WRITE_SIZE, sources {cur})"
 
 
 def cpu_baseline(config, budget_s):
@@ -365,6 +402,9 @@ def leg(name, fn, *a, **kw):
 
 def main():
     args = parse()
+    if args.source_hash:
+        print(traffic_source_hash(), flush=True)
+        return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
@@ -415,7 +455,7 @@ def main():
     s_q = q.shape[0]
     s_kv = k.shape[0]
     alg_bytes = (2 * s_q + 2 * s_kv) * n * d * 2      # Q + O + K + V once, bf16
-    traffic = profile_traffic(cfg)
+    traffic, traffic_src = profile_traffic(cfg)
     result = {
         "metric": "window-attn TFLOP/s & % MFMA peak @2K (21.6k tok); ms per SR-DiT 5B step",
         "value": round(tflops, 2),
@@ -436,6 +476,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "algorithmic_bytes": alg_bytes,
                      "algorithmic_hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1)},
         "wall_s_timed_region": round(wall, 4),
