@@ -55,6 +55,8 @@ def parse():
                     help="rough budget for the CPU baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run the library's 16-byte copy kernel over BYTES (counter calibration)")
+    ap.add_argument("--no-comparator", action="store_true",
+                    help="skip the torch gather + SDPA comparator on the GPU")
     ap.add_argument("--source-hash", action="store_true",
                     help="only print the hash of the sources that decide the window kernel's traffic")
     return ap.parse_args()
@@ -173,8 +175,26 @@ def cpu_baseline(config, budget_s):
                 break
     except OSError:
         cpu_model = platform.processor()
+    # The CPU configuration itself (c1: 3x16x16, 768 tokens), every window, timed
+    # whole: the reference's CPU-runnable case.
+    q1, k1, v1, _, _ = wl.make_window_inputs("c1", torch.float32, "cpu", seed=0)
+    q1, k1, v1 = q1[0], k1[0], v1[0]
+    spec1 = wl.window_spec("c1")
+    g1 = obg.Geometry(**{f: getattr(spec1, f) for f in obg.Geometry.__dataclass_fields__})
+    plan1 = ogt.GatherPlan(g1)
+    flops1 = sum(4 * len(a) * len(b) * wl.HEAD_DIM for a, b in obg.windows(g1)) * wl.N_HEADS
+    t1 = []
+    for i in range(23):
+        t0 = time.perf_counter()
+        ogt.gather_attend(plan1, q1, k1, v1)
+        if i >= 3:
+            t1.append(time.perf_counter() - t0)
+    med1 = statistics.median(t1)
+    c1_full = {"ms": round(med1 * 1e3, 3), "tflops": round(flops1 / med1 / 1e12, 4),
+               "useful_gflop": round(flops1 / 1e9, 3), "windows": len(obg.windows(g1)),
+               "runs": len(t1), "workload": "c1 3x16x16 (768 tokens), 24 heads x 128, fp32, all windows"}
     return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", "c1_full": c1_full,
             "sample": (f"{config} query frame {frame}: {len(sample)} windows x 24 heads, fp32, "
                        f"{flops / 1e9:.2f} GFLOP useful, median of {len(times)} runs "
                        f"{med * 1e3:.1f} ms; os.cpu_count()={os.cpu_count()}; {cpu_model}")}
@@ -388,6 +408,107 @@ def production_window(steps, warmup=3):
     return res
 
 
+def gather_buckets(plan, H, W):
+    """Token indices of every window of a plain plan without an anchor prefix,
+    bucketed by shape: a list of ([Nw, Lq], [Nw, Lkv]) int64 CPU tensors.  Query
+    tokens are the row's query cuboid (fields 0-5), keys its KV cuboid (fields
+    6-11), t-major then row then column on an H x W grid."""
+    import torch
+    L = H * W
+
+    def cuboid(t0, tl, h0, hl, w0, wl_):
+        t = torch.arange(t0, t0 + tl).view(-1, 1, 1) * L
+        r = torch.arange(h0, h0 + hl).view(1, -1, 1) * W
+        cc = torch.arange(w0, w0 + wl_).view(1, 1, -1)
+        return (t + r + cc).reshape(-1)
+
+    buckets = {}
+    for row in plan["params"].tolist():
+        qi = cuboid(row[0], row[1], row[2], row[4], row[3], row[5])
+        ki = cuboid(row[6], row[7], row[8], row[9], row[10], row[11])
+        if qi.numel() == 0 or ki.numel() == 0:
+            continue
+        b = buckets.setdefault((qi.numel(), ki.numel()), ([], []))
+        b[0].append(qi)
+        b[1].append(ki)
+    return [(torch.stack(a), torch.stack(b)) for a, b in buckets.values()]
+
+
+def gpu_gather_comparator(config, steps, warmup=2):
+    """The reference's gather path (attention.py:650-687: per-window token gather,
+    then dense attention per window) restated in torch on the GPU, in bf16, as the
+    on-box comparator for the fused kernel.  Windows are bucketed by (Lq, Lkv) and
+    their token indices built once outside the timed region; each step gathers Q,
+    K and V per bucket, runs torch's fused SDPA on it and scatters the outputs.
+    Only the flash or memory-efficient SDPA backends are used (never the math
+    path in bf16); with neither available the leg reports that instead of a time."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from sr_dit import blockgrid_hip as bgh
+    from sr_dit import workloads as wl
+
+    dev = torch.device("cuda:0")
+    c = wl.WINDOW_CONFIGS[config]
+    spec = wl.window_spec(config)
+    plan = bgh.build_plan(spec)
+    if plan["p_stride"] != bgh.P_PLAIN or plan.get("hr_base", 0):
+        return {"skipped": "plain plans without an anchor only"}
+    H, W = c["h"], c["w"]
+    L = H * W
+    q, k, v, kc, vc = wl.make_window_inputs(config, torch.bfloat16, dev, seed=0)
+    q, k, v = q[0].contiguous(), k[0], v[0]
+    if kc is not None:
+        k, v = torch.cat([kc[0], k]), torch.cat([vc[0], v])
+    k, v = k.contiguous(), v.contiguous()
+
+    groups = [(a.to(dev), b.to(dev)) for a, b in gather_buckets(plan, H, W)]
+    out = torch.empty_like(q)
+    n, d = q.shape[1], q.shape[2]
+
+    def step():
+        for qi, ki in groups:
+            nw, lq = qi.shape
+            lkv = ki.shape[1]
+            qg = q.index_select(0, qi.reshape(-1)).view(nw, lq, n, d).transpose(1, 2)
+            kg = k.index_select(0, ki.reshape(-1)).view(nw, lkv, n, d).transpose(1, 2)
+            vg = v.index_select(0, ki.reshape(-1)).view(nw, lkv, n, d).transpose(1, 2)
+            og = F.scaled_dot_product_attention(qg.contiguous(), kg.contiguous(), vg.contiguous())
+            out.index_copy_(0, qi.reshape(-1), og.transpose(1, 2).reshape(nw * lq, n, d))
+
+    backend = None
+    for name, bk in (("flash", SDPBackend.FLASH_ATTENTION),
+                     ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel([bk]):
+                step()
+            torch.cuda.synchronize()
+            backend = (name, bk)
+            break
+        except RuntimeError:
+            continue
+    if backend is None:
+        return {"skipped": "neither the flash nor the memory-efficient SDPA backend runs here"}
+    stream = torch.cuda.current_stream(dev)
+    with sdpa_kernel([backend[1]]):
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = wl.plan_useful_flops(plan)
+    return {"workload": config, "sdpa_backend": backend[0], "buckets": len(groups),
+            "ms_per_step": round(ms, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "note": "torch gather + SDPA restatement of the reference's gather path, bf16, "
+                    "index tables built outside the timed region"}
+
+
 def leg(name, fn, *a, **kw):
     """Run one measurement leg inside a named range (a roctx range under rocprofv3
     --marker-trace), so kernel traces can be split by leg."""
@@ -481,6 +602,11 @@ def main():
                      "algorithmic_hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1)},
         "wall_s_timed_region": round(wall, 4),
     }
+    if not args.no_comparator:
+        result["gpu_comparator"] = leg("gpu_comparator", gpu_gather_comparator, cfg, 5)
+        if result["gpu_comparator"].get("ms_per_step"):
+            result["gpu_comparator"]["speedup_of_kernel"] = round(
+                result["gpu_comparator"]["ms_per_step"] / ms, 2)
     if not args.no_prod:
         result["production_window"] = leg("production_window", production_window, 20)
     if not (args.no_step and args.no_stream):
