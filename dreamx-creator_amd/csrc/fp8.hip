@@ -237,42 +237,133 @@ __device__ __forceinline__ float bf16_rt(float x) {
   return __uint_as_float(b << 16);
 }
 
-// The FFN's hidden activation h = bf16(gelu_tanh(x)) for x [M, K] bf16 (the
-// first Linear's bf16 output), then its per-tensor quantisation: pass 1 writes
-// h (in place over x when h == x) and reduces max |h| into amax_ws; pass 2 is
-// the per-tensor quantiser of h.  GELU is evaluated once per element.
-__global__ __launch_bounds__(256) void gelu_amax_kernel(const uint16_t* x, int64_t M, int64_t K,
-                                                        int64_t ldx, uint16_t* h, int64_t ldh,
-                                                        uint32_t* __restrict__ amax_ws) {
-  __shared__ uint32_t part[4];
+// GELU through a table.  The FFN's hidden activation h = bf16(gelu_tanh(x)) is
+// a function of the 16 bits of a bf16 x, so the per-tensor GELU quantiser looks
+// h up in a 65,536-entry table instead of evaluating tanhf per element (the
+// passes were bound by tanhf).  gelu_lut_build_kernel writes the table (one
+// entry per thread, the same gelu_tanh and bf16 rounding as the GEMM epilogue);
+// each workgroup of the two passes copies it into LDS (128 KB: one workgroup
+// per CU) and looks every element up there.  Pass 1 reduces max |h| (and stores
+// h when asked); pass 2 quantises h with the scale of that amax.
+constexpr int LUT_N = 65536;
+constexpr int LUT_WAVES = 16;  // wavefronts per workgroup of the table passes
+
+__global__ __launch_bounds__(256) void gelu_lut_build_kernel(uint16_t* __restrict__ lut,
+                                                             uint32_t* __restrict__ amax_ws) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // < LUT_N / 2: entries 2i, 2i + 1
+  typedef float f32x2v __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+  const float x0 = __uint_as_float(static_cast<uint32_t>(2 * i) << 16);
+  const float x1 = __uint_as_float(static_cast<uint32_t>(2 * i + 1) << 16);
+  reinterpret_cast<uint32_t*>(lut)[i] =
+      __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{gelu_tanh(x0), gelu_tanh(x1)},
+                                                           bf16x2v));
+  if (i == 0) *amax_ws = 0u;
+}
+
+__device__ __forceinline__ void load_lut_to_lds(uint16_t* lds, const uint16_t* __restrict__ lut) {
+  const uint4* src = reinterpret_cast<const uint4*>(lut);
+  uint4* dst = reinterpret_cast<uint4*>(lds);
+  for (int i = threadIdx.x; i < LUT_N / 8; i += blockDim.x) dst[i] = src[i];
+  __syncthreads();
+}
+
+// h for the 8 bf16 of one 16-byte chunk: four words of two table entries each.
+__device__ __forceinline__ uint4 lut8(const uint16_t* lds, uint4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = static_cast<uint32_t>(lds[w[i] & 0xffffu]) | (static_cast<uint32_t>(lds[w[i] >> 16]) << 16);
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__device__ __forceinline__ uint32_t abs_bits_max_bf16x8(uint4 h, uint32_t m) {
+  const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = max(m, max((w[i] & 0x7fffu) << 16, w[i] & 0x7fff0000u));
+  return m;
+}
+
+__global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_amax_kernel(
+    const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx, uint16_t* __restrict__ h,
+    int64_t ldh, const uint16_t* __restrict__ lut, uint32_t* __restrict__ amax_ws) {
+  __shared__ __attribute__((aligned(16))) uint16_t tab[LUT_N];
+  __shared__ uint32_t part[LUT_WAVES];
+  load_lut_to_lds(tab, lut);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t nchunk = K >> 3;
   uint32_t amax = 0;
-  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < M; row += (int64_t)gridDim.x * 4) {
-    const uint16_t* xr = x + row * ldx;
-    uint4* hr = reinterpret_cast<uint4*>(h + row * ldh);
-    for (int64_t c = lane; c < nchunk; c += 64) {
-      float f[8];
-      Load8<uint16_t>::get(xr, c, f);
-      uint32_t w[4];
+  for (int64_t row = (int64_t)blockIdx.x * LUT_WAVES + wave; row < M;
+       row += (int64_t)gridDim.x * LUT_WAVES) {
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    uint4* hr = h ? reinterpret_cast<uint4*>(h + row * ldh) : nullptr;
+    // QU chunks per lane in flight; a clamped index re-reads a chunk already
+    // counted, which leaves the max unchanged
+    for (int64_t c0 = lane; c0 < nchunk; c0 += 64 * QU) {
+      uint4 v[QU];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        typedef float f32x2v __attribute__((ext_vector_type(2)));
-        typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-        w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
-                                                f32x2v{gelu_tanh(f[2 * i]), gelu_tanh(f[2 * i + 1])},
-                                                bf16x2v));
-        f[2 * i] = __uint_as_float(w[i] << 16);
-        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      for (int u = 0; u < QU; ++u) {
+        const int64_t c = c0 + 64 * u;
+        v[u] = xr[c < nchunk ? c : nchunk - 1];
       }
-      hr[c] = make_uint4(w[0], w[1], w[2], w[3]);
-      amax = abs_bits_max8(f, amax);
+#pragma unroll
+      for (int u = 0; u < QU; ++u) {
+        const uint4 hv = lut8(tab, v[u]);
+        amax = abs_bits_max_bf16x8(hv, amax);
+        const int64_t c = c0 + 64 * u;
+        if (hr && c < nchunk) hr[c] = hv;
+      }
     }
   }
   amax = wave_umax(amax);
   if (lane == 0) part[wave] = amax;
   __syncthreads();
-  if (threadIdx.x == 0) atomicMax(amax_ws, max(max(part[0], part[1]), max(part[2], part[3])));
+  if (threadIdx.x == 0) {
+    uint32_t m = part[0];
+#pragma unroll
+    for (int w = 1; w < LUT_WAVES; ++w) m = max(m, part[w]);
+    atomicMax(amax_ws, m);
+  }
+}
+
+__global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_quant_kernel(
+    const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
+    const uint16_t* __restrict__ lut, uint8_t* __restrict__ xq, float* __restrict__ scale,
+    const uint32_t* __restrict__ amax_ws) {
+  __shared__ __attribute__((aligned(16))) uint16_t tab[LUT_N];
+  load_lut_to_lds(tab, lut);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float s = scale_from_amax_bits(*amax_ws);
+  const SharedDivisor sd(s);
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
+  const int64_t nchunk = K >> 3;
+  for (int64_t row = (int64_t)blockIdx.x * LUT_WAVES + wave; row < M;
+       row += (int64_t)gridDim.x * LUT_WAVES) {
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
+    for (int64_t c0 = lane; c0 < nchunk; c0 += 64 * QU) {
+      uint4 v[QU];
+#pragma unroll
+      for (int u = 0; u < QU; ++u) {
+        const int64_t c = c0 + 64 * u;
+        v[u] = xr[c < nchunk ? c : nchunk - 1];
+      }
+#pragma unroll
+      for (int u = 0; u < QU; ++u) {
+        const uint4 hv = lut8(tab, v[u]);
+        const uint32_t w[4] = {hv.x, hv.y, hv.z, hv.w};
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f[2 * i] = __uint_as_float(w[i] << 16);
+          f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+        const int64_t c = c0 + 64 * u;
+        if (c < nchunk) qr[c] = to_e4m3x8(f, sd);
+      }
+    }
+  }
 }
 
 // The epilogue of one wavefront's NI x NJ blocks of 32 x 32: acc[i][j] is
@@ -635,25 +726,75 @@ extern "C" int srdit_fp8_quant_apply(const void* x, int64_t M, int64_t K, int64_
   });
 }
 
+// The GELU table: one static 128 KB array per device, addressed through
+// hipGetSymbolAddress (taken once per device).  Every call rewrites it before
+// its passes read it, in stream order; calls on other streams of the device
+// write the same values, so overlapping calls read correct entries.
+static __device__ __align__(256) uint16_t gelu_lut_table[srdit::LUT_N];
+
+namespace srdit {
+namespace {
+std::mutex g_lut_mu;
+void* g_lut_dev[64] = {};
+int g_cus_dev[64] = {};
+
+int gelu_lut_of_current_device(void** out, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  SRDIT_REQUIRE(e == hipSuccess, "%s: hipGetDevice failed: %s", who, hipGetErrorString(e));
+  SRDIT_REQUIRE(dev >= 0 && dev < 64, "%s: device %d out of range", who, dev);
+  std::lock_guard<std::mutex> lock(g_lut_mu);
+  if (!g_lut_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(gelu_lut_table));
+    if (e != hipSuccess || !p) {
+      set_error("%s: hipGetSymbolAddress(gelu_lut_table) failed on device %d: %s", who, dev,
+                hipGetErrorString(e));
+      return SRDIT_EHIP;
+    }
+    g_lut_dev[dev] = p;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    g_cus_dev[dev] = n;
+  }
+  *out = g_lut_dev[dev];
+  return SRDIT_OK;
+}
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(g_lut_mu);
+  return g_cus_dev[dev] > 0 ? g_cus_dev[dev] : 256;
+}
+}  // namespace
+}  // namespace srdit
+
 extern "C" int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx,
                                            void* h, int64_t ldh, void* xq, float* scale,
                                            uint32_t* amax_ws, void* stream) {
   if (int rc = check_quant_args("srdit_fp8_quant_tensor_gelu", x, M, K, ldx, xq, scale)) return rc;
-  SRDIT_REQUIRE(amax_ws && h, "srdit_fp8_quant_tensor_gelu: null amax workspace or h");
-  SRDIT_REQUIRE(aligned16(h) && ldh >= K && ldh % 8 == 0 && (h == x ? ldh == ldx : true),
-                "srdit_fp8_quant_tensor_gelu: h must be 16-byte aligned with ldh >= K, ldh %% 8 == 0 "
-                "(ldh == ldx in place)");
+  SRDIT_REQUIRE(amax_ws, "srdit_fp8_quant_tensor_gelu: null amax workspace");
+  SRDIT_REQUIRE(!h || (aligned16(h) && ldh >= K && ldh % 8 == 0 && h != x),
+                "srdit_fp8_quant_tensor_gelu: h must be null, or 16-byte aligned with ldh >= K, "
+                "ldh %% 8 == 0, and not x");
+  void* lut = nullptr;
+  if (int rc = gelu_lut_of_current_device(&lut, "srdit_fp8_quant_tensor_gelu")) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t rows4 = (M + 3) / 4;
-  const unsigned blocks = (unsigned)(rows4 < 4096 ? rows4 : 4096);
-  clear_u32_kernel<<<1, 1, 0, s>>>(amax_ws);
-  SRDIT_LAUNCH_CHECK("clear_u32_kernel");
-  gelu_amax_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(x), M, K, ldx,
-                                          static_cast<uint16_t*>(h), ldh, amax_ws);
-  SRDIT_LAUNCH_CHECK("gelu_amax_kernel");
-  quant_tensor_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(h), M, K, ldh,
-                                                       static_cast<uint8_t*>(xq), scale, amax_ws);
-  SRDIT_LAUNCH_CHECK("quant_tensor_kernel");
+  const int64_t rows16 = (M + LUT_WAVES - 1) / LUT_WAVES;
+  const int cus = device_cu_count();
+  const unsigned blocks = (unsigned)(rows16 < cus ? rows16 : cus);  // one workgroup per CU
+  gelu_lut_build_kernel<<<LUT_N / 512, 256, 0, s>>>(static_cast<uint16_t*>(lut), amax_ws);
+  SRDIT_LAUNCH_CHECK("gelu_lut_build_kernel");
+  gelu_lut_amax_kernel<<<blocks, 64 * LUT_WAVES, 0, s>>>(
+      static_cast<const uint16_t*>(x), M, K, ldx, static_cast<uint16_t*>(h), ldh,
+      static_cast<const uint16_t*>(lut), amax_ws);
+  SRDIT_LAUNCH_CHECK("gelu_lut_amax_kernel");
+  gelu_lut_quant_kernel<<<blocks, 64 * LUT_WAVES, 0, s>>>(
+      static_cast<const uint16_t*>(x), M, K, ldx, static_cast<const uint16_t*>(lut),
+      static_cast<uint8_t*>(xq), scale, amax_ws);
+  SRDIT_LAUNCH_CHECK("gelu_lut_quant_kernel");
   return SRDIT_OK;
 }
 

@@ -280,15 +280,18 @@ def fp8_linear_tensor_static(x, w, w_scale, bias, out):
 
 
 def fp8_quant_tensor_gelu(x, xq, scale, amax_ws, h=None):
-    """h = bf16(gelu_tanh(x)) (into x itself when h is None), then the per-tensor
-    e4m3 quantisation of h into xq / scale."""
+    """The per-tensor e4m3 quantisation of h = bf16(gelu_tanh(x)) into xq / scale;
+    h itself is also written when a buffer other than x is given."""
     M, K, ldx, dt = _quant_args(x, xq)
     if dt != 0:
         raise ValueError("fp8_quant_tensor_gelu: x must be bf16")
-    h = x if h is None else h
-    if h.dtype != torch.bfloat16 or tuple(h.shape) != (M, K) or h.stride(1) != 1:
-        raise ValueError("fp8_quant_tensor_gelu: h must be bf16 shaped like x with unit column stride")
-    rc = load().srdit_fp8_quant_tensor_gelu(_ptr(x), M, K, ldx, _ptr(h), h.stride(0), _ptr(xq),
+    if h is not None:
+        if h.dtype != torch.bfloat16 or tuple(h.shape) != (M, K) or h.stride(1) != 1 or \
+                h.data_ptr() == x.data_ptr():
+            raise ValueError("fp8_quant_tensor_gelu: h must be a bf16 buffer shaped like x "
+                             "(unit column stride), not x itself")
+    rc = load().srdit_fp8_quant_tensor_gelu(_ptr(x), M, K, ldx, _ptr(h),
+                                            h.stride(0) if h is not None else 0, _ptr(xq),
                                             _ptr(scale), _ptr(amax_ws), _stream(x.device))
     _check(rc, "srdit_fp8_quant_tensor_gelu")
 

@@ -218,12 +218,15 @@ int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_row
  * the output (srdit_fp8_quant_apply).  Same layout rules as srdit_fp8_gemm.
  */
 /*
- * The FFN's hidden activation and its per-tensor e4m3 quantiser: writes
- * h = bf16(gelu_tanh(x)) for x [M, K] bf16 (row stride ldx) into h (row stride
- * ldh; h may be x, with ldh == ldx), then quantises h as srdit_fp8_quant_tensor
- * does (same outputs, same workspace rule).  The GELU of models.py:1200-1202 on
- * the first Linear's bf16 output, then the second Linear's per-tensor
- * quantiser (fp8_linear.py:80-130 with one scale).  bf16 only.
+ * The FFN's hidden activation and its per-tensor e4m3 quantiser: quantises
+ * h = bf16(gelu_tanh(x)) for x [M, K] bf16 (row stride ldx) as
+ * srdit_fp8_quant_tensor does (same outputs, same workspace rule).  h is looked
+ * up in a table of all 65,536 bf16 inputs, rebuilt by every call in a static
+ * 128 KB device array (no allocation); x is read twice (amax, then codes) and
+ * not modified.  h (nullable; row stride ldh, not x): also stores h there.  The
+ * GELU of models.py:1200-1202 on the first Linear's bf16 output, then the
+ * second Linear's per-tensor quantiser (fp8_linear.py:80-130 with one scale).
+ * bf16 only.
  */
 int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx, void* h,
                                 int64_t ldh, void* xq, float* scale, uint32_t* amax_ws,

@@ -344,11 +344,11 @@ def test_fused_block_matches_unfused(scaling):
 
 def test_gelu_quantiser_matches_stored_gelu_then_quantiser():
     """srdit_fp8_quant_tensor_gelu: h == torch's bf16(gelu_tanh(x)) and the codes
-    and scale == the per-tensor quantiser of that h, bit for bit, into a separate
-    buffer and in place."""
+    and scale == the per-tensor quantiser of that h, bit for bit, with h stored
+    into a separate buffer and without h (x left untouched)."""
     from sr_dit import _lib
     g = torch.Generator("cpu").manual_seed(12)
-    for M, K in ((300, 384), (2048, 14336)):
+    for M, K in ((300, 384), (2048, 14336), (37, 8)):
         x = (torch.randn(M, K, generator=g) * 3).to(torch.bfloat16).to(DEV)
         h = F.gelu(x.float(), approximate="tanh").to(torch.bfloat16)
         want_q = torch.empty(M, K, dtype=F8, device=DEV)
@@ -364,8 +364,32 @@ def test_gelu_quantiser_matches_stored_gelu_then_quantiser():
         assert torch.equal(hbuf, h)
         assert torch.equal(got_s, want_s), (got_s.item(), want_s.item())
         assert torch.equal(got_q.view(torch.uint8), want_q.view(torch.uint8))
-        xi = x.clone()
-        _lib.fp8_quant_tensor_gelu(xi, got_q, got_s, ws2)               # in place
+        assert torch.equal(ws2, ws)                                      # the amax word
+        x0 = x.clone()
+        got_q.zero_()
+        _lib.fp8_quant_tensor_gelu(x, got_q, got_s, ws2)                # no h
         torch.cuda.synchronize()
-        assert torch.equal(xi, h)
+        assert torch.equal(x, x0)
+        assert torch.equal(got_s, want_s)
         assert torch.equal(got_q.view(torch.uint8), want_q.view(torch.uint8))
+
+
+def test_gelu_table_covers_every_bf16_value():
+    """The GELU table against torch's GELU for all 65,536 bf16 inputs: finite
+    outputs bit for bit, NaN exactly where torch gives NaN."""
+    from sr_dit import _lib
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = bits.reshape(128, 512).to(DEV)
+    want = F.gelu(x.float(), approximate="tanh").to(torch.bfloat16)
+    h = torch.empty_like(x)
+    q = torch.empty(128, 512, dtype=F8, device=DEV)
+    sc = torch.empty(1, dtype=torch.float32, device=DEV)
+    ws = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _lib.fp8_quant_tensor_gelu(x, q, sc, ws, h=h)
+    torch.cuda.synchronize()
+    nan_w, nan_h = torch.isnan(want), torch.isnan(h)
+    assert torch.equal(nan_w, nan_h)
+    ok = ~nan_w
+    assert torch.equal(h[ok].view(torch.int16), want[ok].view(torch.int16))
+    print(f"[metrics] gelu table: {int(ok.sum())} finite-or-inf outputs bit-exact, "
+          f"{int(nan_w.sum())} NaN", flush=True)
