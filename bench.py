@@ -55,6 +55,9 @@ def parse():
                     help="rough budget for the CPU baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run the library's 16-byte copy kernel over BYTES (counter calibration)")
+    ap.add_argument("--settle-ms", type=float, default=100.0,
+                    help="untimed launches of the c3 step for this long before the warm-up "
+                         "(0: none), so the timed steps see the sustained-load clock")
     ap.add_argument("--no-comparator", action="store_true",
                     help="skip the torch gather + SDPA comparator on the GPU")
     ap.add_argument("--source-hash", action="store_true",
@@ -555,6 +558,20 @@ def main():
                               n=n, d=d)
 
     torch.cuda.nvtx.range_push("window_" + cfg)
+    # Settle: untimed launches of the same step for --settle-ms of wall time before
+    # the warm-up.  The GPU raises its clock over the first few tens of
+    # milliseconds of sustained load (c3 with 5 warm-up launches: 477 us per
+    # timed launch; with 50: 400 us), so without it the timed steps would see a
+    # clock the GPU does not hold under load.  Reported in the JSON line.
+    step()
+    torch.cuda.synchronize()  # first launch: module load and table uploads
+    settle_n, t_settle = 1, time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms and settle_n < 4096:
+        for _ in range(16):
+            step()
+        settle_n += 16
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_settle
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -601,6 +618,9 @@ def main():
                      "algorithmic_bytes": alg_bytes,
                      "algorithmic_hbm_gbs": round(alg_bytes / (ms * 1e-3) / 1e9, 1)},
         "wall_s_timed_region": round(wall, 4),
+        "settle": {"launches": settle_n, "wall_ms": round(settle_s * 1e3, 1),
+                   "note": "untimed launches of the same step before the warm-up steps, so the "
+                           "timed steps run at the clock the GPU holds under sustained load"},
     }
     if not args.no_comparator:
         result["gpu_comparator"] = leg("gpu_comparator", gpu_gather_comparator, cfg, 5)
