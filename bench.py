@@ -274,10 +274,12 @@ def refiner_step(model, build_s, replays, warmup):
             b.record(stream)
         torch.cuda.synchronize()
         times = [a.elapsed_time(b) for a, b in ev]
+        same_last = bool(torch.equal(y, want))  # the output of the last timed replay
     ms = statistics.median(times)
     return {"ms_per_step": round(ms, 3), "mean_ms": round(statistics.fmean(times), 3),
             "min_ms": round(min(times), 3), "max_ms": round(max(times), 3), "replays": replays,
-            "eager_ms": round(eager_ms, 3), "graph_equals_eager": same,
+            "eager_ms": round(eager_ms, 3), "graph_equals_eager": same and same_last,
+            "graph_first_replay_equals_eager": same, "graph_last_replay_equals_eager": same_last,
             "hip_graph": True, "layers": layers, "tokens": s_tok, "context_tokens": cfg.text_len,
             "scope": "time + text embeddings, patch embedding, 30 blocks, head, unpatchify",
             "linears": "fp8 e4m3, " + ("per-tensor" if scaling_of(model) == "tensor"
