@@ -144,7 +144,7 @@ __global__ __launch_bounds__(256) void amax_kernel(const T* __restrict__ x, int6
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t m = max(max(part[0], part[1]), max(part[2], part[3]));
-    atomicMax(amax_ws, m);
+    raise_max_word(amax_ws, m);
   }
 }
 
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_amax_kernel(
     uint32_t m = part[0];
 #pragma unroll
     for (int w = 1; w < LUT_WAVES; ++w) m = max(m, part[w]);
-    atomicMax(amax_ws, m);
+    raise_max_word(amax_ws, m);
   }
 }
 
@@ -435,7 +435,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16_t 
   if (AMAX) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, o));
-    if (lane == 0) atomicMax(g.amax_out, amax);
+    if (lane == 0) raise_max_word(g.amax_out, amax);
   }
 }
 

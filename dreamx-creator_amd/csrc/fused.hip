@@ -70,9 +70,9 @@ __global__ void clear_word_kernel(uint32_t* p) { *p = 0u; }
 // keeps its <= 8 chunks of the row in registers, so the row is read once;
 // otherwise the mean, variance and output passes re-read it (L1/L2 hits).
 // Per lane the chunks are summed in the order c = lane, lane + 64, ..., as the
-// output pass visits them.  The amax is reduced per workgroup, then one
-// atomicMax per workgroup.  VEC: scale and shift are 16-byte aligned and read
-// as float4.
+// output pass visits them.  The amax is reduced per workgroup, then raises
+// the word once per workgroup (raise_max_word).  VEC: scale and shift are
+// 16-byte aligned and read as float4.
 template <bool AFFINE, bool MOD, bool AMAX, bool CACHED, bool VEC>
 __global__ __launch_bounds__(256) void ln_modulate_kernel(
     const uint16_t* __restrict__ x, int64_t M, int K, int64_t ldx, const uint16_t* __restrict__ w,
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(
     if (lane == 0) wmax[threadIdx.x >> 6] = am;
     __syncthreads();
     if (threadIdx.x == 0)
-      atomicMax(amax_ws, max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3])));
+      raise_max_word(amax_ws, max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3])));
   }
 }
 

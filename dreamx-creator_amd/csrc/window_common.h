@@ -199,7 +199,7 @@ __device__ __forceinline__ LaneOff<D> make_lane_offsets(int wave) {
 // the frame kernel are all this formula with their own grid.
 // Max |value| of the output, as fp32 bits (non-negative floats order like their
 // bits; a NaN sorts above infinity, so it wins as in torch's amax): the
-// wavefront's maximum goes to *amax with one atomicMax from lane 0.
+// wavefront's maximum goes to *amax from lane 0 (raise_max_word).
 template <typename H2>
 __device__ __forceinline__ uint32_t abs_bits2(H2 v) {
   const f32x2_t f = __builtin_convertvector(v, f32x2_t);
@@ -209,7 +209,7 @@ __device__ __forceinline__ uint32_t abs_bits2(H2 v) {
 __device__ __forceinline__ void wave_amax_out(uint32_t* amax, uint32_t m) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), o)));
-  if ((threadIdx.x & 63) == 0) atomicMax(amax, m);
+  if ((threadIdx.x & 63) == 0) raise_max_word(amax, m);
 }
 
 // Frame layout of a streaming KV cache kept in place: R ring slots holding the
