@@ -4,6 +4,10 @@
 //                  and, optionally, the max |out| (float bits) into an amax word
 //                  for a per-tensor fp8 quantiser of `out`
 //   residual_gate  out = bf16( f32(x) + f32(y) * gate )
+//   residual_ln_modulate
+//                  x_out = residual_gate(x, y, gate), then ln_modulate(x_out)
+//                  from the same registers: one pass for the gated residual
+//                  and the LayerNorm that reads the new residual stream
 //   rmsnorm_rope   out = RoPE( bf16( f32(bf16(x * rsqrt(mean(x^2) + eps))) * f32(w) ) )
 //
 // They restate, op for op, the elementwise chains of the reference block
@@ -73,11 +77,24 @@ __global__ void clear_word_kernel(uint32_t* p) { *p = 0u; }
 // output pass visits them.  The amax is reduced per workgroup, then raises
 // the word once per workgroup (raise_max_word).  VEC: scale and shift are
 // 16-byte aligned and read as float4.
-template <bool AFFINE, bool MOD, bool AMAX, bool CACHED, bool VEC>
+// RES (CACHED only): the row is first the gated residual x + y * gate (16-byte
+// aligned fp32 gate [K]), computed as residual_gate_kernel computes it, stored
+// to xo (row stride ldxo) and kept in registers for the LayerNorm.
+struct ResidualIn {
+  const uint16_t* y;
+  int64_t ldy;
+  const float* gate;
+  uint16_t* xo;
+  int64_t ldxo;
+};
+
+template <bool AFFINE, bool MOD, bool AMAX, bool CACHED, bool VEC, bool RES = false>
 __global__ __launch_bounds__(256) void ln_modulate_kernel(
     const uint16_t* __restrict__ x, int64_t M, int K, int64_t ldx, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ b, const float* __restrict__ scale, const float* __restrict__ shift,
-    float eps, uint16_t* __restrict__ out, int64_t ldo, uint32_t* __restrict__ amax_ws) {
+    float eps, uint16_t* __restrict__ out, int64_t ldo, uint32_t* __restrict__ amax_ws,
+    ResidualIn res = ResidualIn{}) {
+  static_assert(!RES || CACHED, "the residual prologue keeps the row in registers");
   constexpr int CPL = 8;  // cached chunks per lane
   const int lane = threadIdx.x & 63;
   const int nc = K >> 3;
@@ -86,7 +103,33 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(
        row += static_cast<int64_t>(gridDim.x) * 4) {
     const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
     uint4 rb[CACHED ? CPL : 1];
-    if (CACHED) {
+    if constexpr (RES) {
+      const uint4* yr = reinterpret_cast<const uint4*>(res.y + row * res.ldy);
+      uint4 yb[CPL];
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = lane + 64 * i;
+        rb[i] = c < nc ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+        yb[i] = c < nc ? yr[c] : make_uint4(0u, 0u, 0u, 0u);
+      }
+      uint4* xor_ = reinterpret_cast<uint4*>(res.xo + row * res.ldxo);
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nc) {
+          float xf[8], yf[8], o[8];
+          unpack_bf16x8(rb[i], xf);
+          unpack_bf16x8(yb[i], yf);
+          const float4 g0 = reinterpret_cast<const float4*>(res.gate)[2 * c];
+          const float4 g1 = reinterpret_cast<const float4*>(res.gate)[2 * c + 1];
+          const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = __fadd_rn(xf[e], __fmul_rn(yf[e], g[e]));
+          rb[i] = pack_bf16x8(o);
+          xor_[c] = rb[i];
+        }
+      }
+    } else if (CACHED) {
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
         const int c = lane + 64 * i;
@@ -293,19 +336,24 @@ int check_rows(const char* who, const void* x, int64_t M, int K, int64_t ldx, co
 
 using namespace srdit;
 
-extern "C" int srdit_ln_modulate(const void* x, int64_t M, int K, int64_t ldx, const void* ln_w,
-                                 const void* ln_b, const float* scale, const float* shift, float eps,
-                                 void* out, int64_t ldo, uint32_t* amax_ws, void* stream) {
-  if (int rc = check_rows("srdit_ln_modulate", x, M, K, ldx, out, ldo)) return rc;
-  SRDIT_REQUIRE((ln_w == nullptr) == (ln_b == nullptr),
-                "srdit_ln_modulate: give both affine tensors or neither");
+namespace srdit {
+namespace {
+
+// The LayerNorm launch shared by srdit_ln_modulate and, with `res`, the fused
+// residual of srdit_residual_ln_modulate (which only passes res for K <= 4096).
+int ln_modulate_launch(const char* who, const void* x, int64_t M, int K, int64_t ldx,
+                       const void* ln_w, const void* ln_b, const float* scale, const float* shift,
+                       float eps, void* out, int64_t ldo, uint32_t* amax_ws, hipStream_t s,
+                       const ResidualIn* res) {
+  if (int rc = check_rows(who, x, M, K, ldx, out, ldo)) return rc;
+  SRDIT_REQUIRE((ln_w == nullptr) == (ln_b == nullptr), "%s: give both affine tensors or neither",
+                who);
   SRDIT_REQUIRE((scale == nullptr) == (shift == nullptr),
-                "srdit_ln_modulate: give both modulation tensors or neither");
+                "%s: give both modulation tensors or neither", who);
   SRDIT_REQUIRE((!ln_w || (aligned16(ln_w) && aligned16(ln_b))) &&
                     (!scale || ((reinterpret_cast<uintptr_t>(scale) & 3) == 0 &&
                                 (reinterpret_cast<uintptr_t>(shift) & 3) == 0)),
-                "srdit_ln_modulate: misaligned affine or modulation tensor");
-  hipStream_t s = static_cast<hipStream_t>(stream);
+                "%s: misaligned affine or modulation tensor", who);
   if (amax_ws) {
     clear_word_kernel<<<1, 1, 0, s>>>(amax_ws);
     SRDIT_LAUNCH_CHECK("clear_word_kernel");
@@ -319,14 +367,17 @@ extern "C" int srdit_ln_modulate(const void* x, int64_t M, int K, int64_t ldx, c
   uint16_t* op = static_cast<uint16_t*>(out);
   const bool cached = K <= 4096;
   const bool vec = scale != nullptr && aligned16(scale) && aligned16(shift);
-#define SRDIT_LN_LAUNCH2(A, MO, AM, C, V)                                                      \
-  ln_modulate_kernel<A, MO, AM, C, V><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, bp, scale, shift, \
-                                                             eps, op, ldo, amax_ws)
+  const ResidualIn r = res ? *res : ResidualIn{};
+#define SRDIT_LN_LAUNCH2(A, MO, AM, C, V, R)                                                   \
+  ln_modulate_kernel<A, MO, AM, C, V, R><<<blocks, 256, 0, s>>>(xp, M, K, ldx, wp, bp, scale,  \
+                                                                shift, eps, op, ldo, amax_ws, r)
 #define SRDIT_LN_LAUNCH(A, MO, AM)                                          \
   do {                                                                       \
-    if (cached && vec) SRDIT_LN_LAUNCH2(A, MO, AM, true, true);              \
-    else if (cached) SRDIT_LN_LAUNCH2(A, MO, AM, true, false);               \
-    else SRDIT_LN_LAUNCH2(A, MO, AM, false, false);                          \
+    if (res && vec) SRDIT_LN_LAUNCH2(A, MO, AM, true, true, true);           \
+    else if (res) SRDIT_LN_LAUNCH2(A, MO, AM, true, false, true);            \
+    else if (cached && vec) SRDIT_LN_LAUNCH2(A, MO, AM, true, true, false);  \
+    else if (cached) SRDIT_LN_LAUNCH2(A, MO, AM, true, false, false);        \
+    else SRDIT_LN_LAUNCH2(A, MO, AM, false, false, false);                   \
   } while (0)
   const bool af = ln_w != nullptr, mo = scale != nullptr, am = amax_ws != nullptr;
   if (af && mo && am) SRDIT_LN_LAUNCH(true, true, true);
@@ -341,6 +392,39 @@ extern "C" int srdit_ln_modulate(const void* x, int64_t M, int K, int64_t ldx, c
 #undef SRDIT_LN_LAUNCH2
   SRDIT_LAUNCH_CHECK("ln_modulate_kernel");
   return SRDIT_OK;
+}
+
+}  // namespace
+}  // namespace srdit
+
+extern "C" int srdit_ln_modulate(const void* x, int64_t M, int K, int64_t ldx, const void* ln_w,
+                                 const void* ln_b, const float* scale, const float* shift, float eps,
+                                 void* out, int64_t ldo, uint32_t* amax_ws, void* stream) {
+  return ln_modulate_launch("srdit_ln_modulate", x, M, K, ldx, ln_w, ln_b, scale, shift, eps, out,
+                            ldo, amax_ws, static_cast<hipStream_t>(stream), nullptr);
+}
+
+extern "C" int srdit_residual_ln_modulate(const void* x, const void* y, const float* gate,
+                                          int64_t M, int K, int64_t ldx, int64_t ldy,
+                                          void* x_out, int64_t ldxo, const void* ln_w,
+                                          const void* ln_b, const float* scale,
+                                          const float* shift, float eps, void* out, int64_t ldo,
+                                          uint32_t* amax_ws, void* stream) {
+  const char* who = "srdit_residual_ln_modulate";
+  if (int rc = check_rows(who, x, M, K, ldx, x_out, ldxo)) return rc;
+  SRDIT_REQUIRE(y && gate && aligned16(y) && aligned16(gate) && ldy >= K && ldy % 8 == 0,
+                "%s: y / gate missing or misaligned, or bad ldy", who);
+  SRDIT_REQUIRE(x_out != x && x_out != out && out != x && out != y,
+                "%s: x_out and out must be buffers of their own", who);
+  if (K > 4096) {  // the row does not fit the registers: the two kernels one after the other
+    if (int rc = srdit_residual_gate(x, y, gate, M, K, ldx, ldy, x_out, ldxo, stream)) return rc;
+    return srdit_ln_modulate(x_out, M, K, ldxo, ln_w, ln_b, scale, shift, eps, out, ldo, amax_ws,
+                             stream);
+  }
+  const ResidualIn res{static_cast<const uint16_t*>(y), ldy, gate, static_cast<uint16_t*>(x_out),
+                       ldxo};
+  return ln_modulate_launch(who, x, M, K, ldx, ln_w, ln_b, scale, shift, eps, out, ldo, amax_ws,
+                            static_cast<hipStream_t>(stream), &res);
 }
 
 extern "C" int srdit_residual_gate(const void* x, const void* y, const float* gate, int64_t M, int K,

@@ -55,6 +55,9 @@ SIGNATURES = {
                                    _c_p, _c_i64, _c_p, _c_p]),
     "srdit_residual_gate": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_int, _c_i64, _c_i64, _c_p,
                                      _c_i64, _c_p]),
+    "srdit_residual_ln_modulate": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_int, _c_i64, _c_i64,
+                                            _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_f, _c_p,
+                                            _c_i64, _c_p, _c_p]),
     "srdit_rmsnorm_rope": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_f, _c_p, _c_int, _c_p,
                                     _c_p]),
     "srdit_last_error": (_c_int, [ctypes.c_char_p, _c_int]),
@@ -325,6 +328,19 @@ def residual_gate(x, y, gate, out):
     rc = load().srdit_residual_gate(_ptr(x), _ptr(y), _ptr(gate), M, K, x.stride(0), y.stride(0),
                                     _ptr(out), out.stride(0), _stream(x.device))
     _check(rc, "srdit_residual_gate")
+
+
+def residual_ln_modulate(x, y, gate, x_out, ln_w, ln_b, scale, shift, eps, out, amax_ws=None):
+    """x_out = bf16(x + y * gate), out = ln_modulate(x_out, ...): one pass, the same
+    bits as residual_gate followed by ln_modulate."""
+    for nm, t in (("x", x), ("y", y), ("x_out", x_out), ("out", out)):
+        _bf16_rows(f"residual_ln_modulate {nm}", t)
+    M, K = x.shape
+    rc = load().srdit_residual_ln_modulate(
+        _ptr(x), _ptr(y), _ptr(gate), M, K, x.stride(0), y.stride(0), _ptr(x_out),
+        x_out.stride(0), _ptr(ln_w), _ptr(ln_b), _ptr(scale), _ptr(shift), float(eps), _ptr(out),
+        out.stride(0), _ptr(amax_ws), _stream(x.device))
+    _check(rc, "srdit_residual_ln_modulate")
 
 
 def rmsnorm_rope(x, w, eps, rope_cs, head_dim, out):

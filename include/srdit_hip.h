@@ -271,6 +271,22 @@ int srdit_residual_gate(const void* x, const void* y, const float* gate, int64_t
                         int64_t ldx, int64_t ldy, void* out, int64_t ldo, void* stream);
 
 /*
+ * The gated residual and the LayerNorm that reads its result, in one pass:
+ *   x_out = bf16(f32(x) + f32(y) * gate[k])                 (srdit_residual_gate)
+ *   out   = srdit_ln_modulate(x_out, ln_w, ln_b, scale, shift, eps, amax_ws)
+ * with the same arithmetic as the two calls (bit for bit).  A residual update
+ * of the block followed by the norm that reads the new residual stream
+ * (models.py:1344-1345 then norm3 at :1257; :1257 then norm2 at :1258).
+ * gate fp32 [K] 16-byte aligned; x_out and out are buffers of their own
+ * (neither aliases x, y or the other).  K > 4096 runs the two kernels.
+ */
+int srdit_residual_ln_modulate(const void* x, const void* y, const float* gate, int64_t M, int K,
+                               int64_t ldx, int64_t ldy, void* x_out, int64_t ldxo,
+                               const void* ln_w, const void* ln_b, const float* scale,
+                               const float* shift, float eps, void* out, int64_t ldo,
+                               uint32_t* amax_ws, void* stream);
+
+/*
  * RMSNorm over each row of x [M, K] (bf16, K = heads * head_dim) with weight w
  * (bf16 [K]), then RoPE per head: pair j of a head rotated by
  * (cos, sin) = rope_cs[row][j] (fp32 pairs, [M, head_dim/2]); rope_cs NULL skips

@@ -260,6 +260,37 @@ def test_fused_ln_modulate_and_amax():
                 atol=1e-4 * 2 ** -7)
 
 
+@pytest.mark.parametrize("M,K,affine", [(700, 3072, False), (700, 3072, True), (37, 8, False),
+                                         (129, 1000, True), (64, 6144, False)])
+def test_fused_residual_ln_modulate_matches_the_two_kernels(M, K, affine):
+    """srdit_residual_ln_modulate == srdit_residual_gate then srdit_ln_modulate, bit for
+    bit (both outputs and the amax word), on strided x rows, ragged widths and the
+    K > 4096 path that runs the two kernels."""
+    from sr_dit import _lib
+    g = torch.Generator("cpu").manual_seed(9)
+    x = (torch.randn(M, K + 16, generator=g) * 2).to(torch.bfloat16).to(DEV)[:, 8:8 + K]
+    y = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
+    gate = torch.randn(K, generator=g).to(DEV)
+    w = (torch.randn(K, generator=g) * 0.5 + 1).to(torch.bfloat16).to(DEV) if affine else None
+    b = (torch.randn(K, generator=g) * 0.1).to(torch.bfloat16).to(DEV) if affine else None
+    sc = None if affine else (torch.randn(K, generator=g) * 0.1).to(DEV)
+    sh = None if affine else (torch.randn(K, generator=g) * 0.1).to(DEV)
+    x1_ref = torch.empty(M, K, dtype=torch.bfloat16, device=DEV)
+    out_ref = torch.empty_like(x1_ref)
+    am_ref = torch.full((1,), 5, dtype=torch.int32, device=DEV)
+    _lib.residual_gate(x, y, gate, x1_ref)
+    _lib.ln_modulate(x1_ref, w, b, sc, sh, 1e-6, out_ref, am_ref)
+    x1, out = torch.empty_like(x1_ref), torch.empty_like(x1_ref)
+    am = torch.full((1,), 5, dtype=torch.int32, device=DEV)
+    _lib.residual_ln_modulate(x, y, gate, x1, w, b, sc, sh, 1e-6, out, am)
+    assert torch.equal(x1, (x.float() + y.float() * gate).to(torch.bfloat16))
+    assert torch.equal(x1, x1_ref)
+    assert torch.equal(out, out_ref)
+    assert am.item() == am_ref.item() == out.float().abs().max().view(torch.int32).item()
+    with pytest.raises(RuntimeError):
+        _lib.residual_ln_modulate(x, y, gate, x1, w, b, sc, sh, 1e-6, x1, am)  # out aliases x_out
+
+
 def test_fused_residual_gate_bit_exact():
     from sr_dit import _lib
     g = torch.Generator("cpu").manual_seed(6)
