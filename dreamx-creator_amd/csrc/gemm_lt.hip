@@ -24,8 +24,11 @@
 // operands only, and within it the fastest algorithm.  Most candidates sum K
 // in one order; a stream-K first choice that sums it in another is then
 // passed over when it is alone in its group (10800 x 3072 x 14336: 436 us
-// against 345 us for the fastest of the nine candidates that agree).  A call
-// made during capture before that uses the heuristic's first choice.
+// against 345 us for the fastest of the nine candidates that agree).  The
+// groups are those of the tuning call's operands: on operands that every order
+// sums alike (all zeros, say) the candidates form one group, and the choice is
+// then the fastest of all.  A call made during capture before that uses the
+// heuristic's first choice.
 // Each device also gets one LT_WORKSPACE-byte workspace, allocated by the
 // first call made outside stream capture and kept until the process ends; a
 // call made while its stream is being captured before that uses the plans
