@@ -178,8 +178,8 @@ class StreamingRefiner:
 
     # ---- one model forward --------------------------------------------------
     def _geom(self, key, t_offset):
-        """Geometry of a forward kind: ("harvest", 0), ("anchored", cached) or
-        ("plain", cached)."""
+        """Geometry of a forward kind: ("harvest", 0), ("anchored", cached),
+        ("plain", cached) or ("refresh", cached) (the plain geometry)."""
         kind, cached = key
         kw = dict(chunk=self.chunk, t_offset=t_offset, block_hw=self.block_hw,
                   block_radius_hw=self.block_radius_hw)
@@ -214,6 +214,13 @@ class StreamingRefiner:
         return self.model.forward_embedded(self._lat, self._e, self._e0, self.ctx, geom,
                                            rings=self.rings, cross=self.cross)
 
+    def _run_refresh(self, geom):
+        """The refresh pass: the clean chunk through the stack for its K/V alone
+        (the flow output of causal_inference.py's refresh forward is discarded);
+        the last layer stops once its K/V are in the ring and the head is skipped."""
+        return self.model.forward_embedded(self._lat, self._e, self._e0, self.ctx, geom,
+                                           rings=self.rings, cross=self.cross, kv_only=True)
+
     def _scaled_part(self, ring):
         return ring.anchor_v(0) if self.anchor_mode == "v" else ring.anchor_k(0)
 
@@ -237,7 +244,7 @@ class StreamingRefiner:
         else:
             kv = [(r.anchor_k(0).view(s, dim), r.anchor_v(0).view(s, dim)) for r in self.rings]
         out = self.model.forward_embedded(self._lat_lq, self._e, self._e0, self.ctx, geom,
-                                          cross=self.cross, kv_outs=kv)
+                                          cross=self.cross, kv_outs=kv, kv_only=True)
         if self._repeat:  # LQ (i, j) -> HR (s_h i .. s_h i + s_h - 1, s_w j .. s_w j + s_w - 1)
             f, (h_a, w_a) = self.chunk, self.anchor_hw
             s_h, s_w = self.h // h_a, self.w // w_a
@@ -284,6 +291,12 @@ class StreamingRefiner:
         fn = self._run_anchored if kind == "anchored" else self._run
         return self._launch((kind, self.rings[0].cached), t, latent, t_offset, fn)
 
+    def refresh(self, x0, t_offset):
+        """The cache refresh of a denoised chunk (no anchor): the chunk's K/V at
+        ``context_noise`` go into the rings' current regions (kept by ``commit``)."""
+        self._launch(("refresh", self.rings[0].cached), self.context_noise, x0, t_offset,
+                     self._run_refresh)
+
     def harvest(self, lq, t_offset):
         """LQ-anchor harvest of one chunk (causal_inference.py:426-508): ``lq``
         [in_dim, chunk, 2h, 2w] (the upsampled LR latent; with the native anchor
@@ -323,7 +336,7 @@ class StreamingRefiner:
                 noise = torch.randn(x0.shape, generator=self.gen, device=self.device,
                                     dtype=x0.dtype)
                 noisy = self.sched.add_noise(x0, noise, self.steps[i + 1])
-        self.forward(x0, self.context_noise, t_offset)  # refresh pass, no anchor
+        self.refresh(x0, t_offset)
         self.commit()
         return x0
 

@@ -72,7 +72,9 @@ def test_stream_graph_replays_match_eager(refiner_model):
     noise, ctx, _ = _inputs(refiner_model.cfg, 5)
     rg, g = _stream(refiner_model, noise, ctx, use_graph=True)
     re_, e = _stream(refiner_model, noise, ctx, use_graph=False)
-    assert sorted(rg._graphs) == [("plain", 0), ("plain", 3), ("plain", 6)]  # one per cache length
+    # one step graph and one refresh graph (K/V only) per cache length
+    assert sorted(rg._graphs) == [("plain", 0), ("plain", 3), ("plain", 6),
+                                  ("refresh", 0), ("refresh", 3), ("refresh", 6)]
     for c, (x, y) in enumerate(zip(g, e)):
         err = (x - y).abs().max().item()
         scale = y.abs().max().item()
@@ -117,7 +119,7 @@ def test_stream_lq_anchor_graph_replays_match_eager(refiner_model):
     rg, g = _stream(refiner_model, noise, ctx, lq=lq, use_graph=True, anchor="frame")
     re_, e = _stream(refiner_model, noise, ctx, lq=lq, use_graph=False, anchor="frame")
     assert sorted(rg._graphs) == [("anchored", 0), ("anchored", 3), ("anchored", 6),
-                                  ("harvest", 0), ("plain", 0), ("plain", 3), ("plain", 6)]
+                                  ("harvest", 0), ("refresh", 0), ("refresh", 3), ("refresh", 6)]
     for c, (x, y) in enumerate(zip(g, e)):
         err = (x - y).abs().max().item()
         scale = y.abs().max().item()
