@@ -363,8 +363,10 @@ def production_window(steps, warmup=3):
     """The refiner's shipped window geometry: 4x4-token blocks, radius 3, one 3-frame
     query chunk of 45x80 against 12 KV frames (streaming rule), without an anchor and
     with the LQ anchor in its "frame" and "chunk" alignments (one 45x80 anchor frame per
-    query frame).  Useful TFLOP/s per kernel launch; the single-window kernel runs all
-    three (48-query windows give the grouped kernel nothing to pair)."""
+    query frame).  Useful TFLOP/s per kernel launch.  Without an anchor the launcher
+    packs two 48-query windows into one 64-row tile where neighbours allow; the
+    anchored forms run one window per workgroup (48-query windows give the grouped
+    kernel nothing to pair)."""
     import torch
     from sr_dit import attention as att
     from sr_dit import blockgrid_hip as bgh

@@ -111,12 +111,23 @@ struct FillCursor {
 // every query sees, or 1, per-frame anchor rows (17 fields) where query frame
 // s sees anchor frame s only.  The anchor frames are walked after the HR
 // frames, as extra frame slots with the anchor grid's extent.
+// PACK (one member, AMODE 0): a 64-row tile may hold the queries of two
+// windows whose KV cuboids differ only in their columns (tile table rows of
+// five: window A, A's first query, A's rows in the tile, window B or -1, B's
+// first query).  The tile walks the union of the two column ranges, which the
+// host makes exactly 32 tokens wide, so each 32-key step is one token row of
+// the union and a key's column is its index in the step: every lane sets the
+// scores of the columns outside its own window to -inf, from a 32-bit column
+// set fixed for the whole walk.  A tile of one window (B = -1) walks that
+// window.  A table whose union is not 32 wide gives wrong numbers, never an
+// access outside the tensors (every token index is clamped).
 // Two wavefronts per SIMD: the register budget is 256 per lane (the compiler
 // would otherwise reach for accumulation registers and drop to one).
-template <typename T, int D, int MEMBERS, int AMODE>
+template <typename T, int D, int MEMBERS, int AMODE, bool PACK = false>
 __global__ __launch_bounds__(128 * MEMBERS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void window_group_kernel(GroupArgs a) {
   static_assert(AMODE == 0 || MEMBERS == 1, "anchors run one member per workgroup");
+  static_assert(!PACK || (MEMBERS == 1 && AMODE == 0), "packed tiles run one plain member");
   constexpr int PST = AMODE == 1 ? 17 : 19;  // params row stride
   using E = Elem<T>;
   using V8 = typename E::v8;
@@ -146,20 +157,29 @@ void window_group_kernel(GroupArgs a) {
   const int head = static_cast<int>(task / static_cast<uint32_t>(a.n_groups));
   const int gi = static_cast<int>(task % static_cast<uint32_t>(a.n_groups));
   if (head >= a.n_heads) return;
-  const int32_t* gp = a.groups + 4 * static_cast<int64_t>(gi);
-  int row0 = gp[0], mt0 = gp[1], row1 = gp[2], mt1 = gp[3];
+  const int32_t* gp = a.groups + (PACK ? 5 : 4) * static_cast<int64_t>(gi);
+  int row0 = gp[0], mt0 = gp[1], row1 = PACK ? gp[3] : gp[2], mt1 = PACK ? 0 : gp[3];
+  // PACK: A's rows in the tile (the rest are B's, from B's query pk_qb0 on)
+  const int pk_na = PACK ? min(max(gp[2], 0), 64) : 64, pk_qb0 = PACK ? max(gp[4], 0) : 0;
   row0 = row0 < 0 ? 0 : (row0 >= a.n_w ? a.n_w - 1 : row0);
-  row1 = (MEMBERS == 1 || row1 < 0) ? -1 : (row1 >= a.n_w ? a.n_w - 1 : row1);
+  row1 = ((MEMBERS == 1 && !PACK) || row1 < 0) ? -1 : (row1 >= a.n_w ? a.n_w - 1 : row1);
   const int32_t* p0 = a.params + static_cast<int64_t>(row0) * PST;
   const int32_t* p1 = row1 >= 0 ? a.params + static_cast<int64_t>(row1) * PST : p0;
 
-  // Shared spatial KV extent (member 0's; the host pairs equal extents) and
-  // the two frame ranges.
+  // Shared spatial KV extent (member 0's; the host pairs equal extents; a
+  // packed tile of two windows walks the union of their columns) and the two
+  // frame ranges.
   constexpr int F = AMODE == 1 ? -2 : 0;  // field offset of the HR cuboid in a 17-field row
-  const int kh0 = p0[F + 8], kh_l = p0[F + 9], kw0 = p0[F + 10], kw_l = p0[F + 11];
+  const int kh0 = p0[F + 8], kh_l = p0[F + 9];
+  int kw0 = p0[F + 10], kw_l = p0[F + 11];
+  if (PACK && row1 >= 0) {
+    const int e0 = kw0 + kw_l, b0 = p1[F + 10], e1 = b0 + p1[F + 11];
+    kw0 = min(kw0, b0);
+    kw_l = max(e0, e1) - kw0;
+  }
   const int sp = kh_l > 0 && kw_l > 0 ? kh_l * kw_l : 0;
   const int a0 = p0[F + 6], la = sp > 0 ? max(p0[F + 7], 0) : 0;
-  const int a1 = p1[F + 6], lb = (sp > 0 && row1 >= 0) ? max(p1[F + 7], 0) : 0;
+  const int a1 = p1[F + 6], lb = (!PACK && sp > 0 && row1 >= 0) ? max(p1[F + 7], 0) : 0;
   const int s_lo = max(a0, a1);
   const int nsh = lb > 0 ? max(0, min(a0 + la, a1 + lb) - s_lo) : 0;
   const PrivFrames pf0 = private_frames(a0, la, s_lo, nsh);
@@ -187,8 +207,25 @@ void window_group_kernel(GroupArgs a) {
   }
   const int q_sp = qh_l * qw_l;
   const int lq = q_tl * q_sp;
-  const int m0 = 64 * my_mt;
+  // PACK: A's rows start at its query mt0 (not an m-tile); B's query geometry
+  const int m0 = PACK ? mt0 : 64 * my_mt;
   const bool has_member = my_row >= 0 && qh_l > 0 && qw_l > 0 && q_tl > 0 && m0 >= 0 && m0 < lq;
+  // B's query geometry is read where it is used (the prologue's Q fills and
+  // the epilogue's O stores) through an opaque copy of its row pointer, so it
+  // is not held in registers across the walk: the kernel sits at its register
+  // limit.
+  struct QGeo {
+    int t0, h0, w0, hl, wl, lq;
+  };
+  auto b_geo = [&]() __attribute__((always_inline)) -> QGeo {
+    const int32_t* pb = p1;
+    asm volatile("" : "+s"(pb));
+    QGeo g;
+    g.t0 = pb[0]; g.h0 = pb[2]; g.w0 = pb[3];
+    g.hl = max(pb[4], 1); g.wl = max(pb[5], 1);
+    g.lq = (PACK && row1 >= 0) ? max(pb[1], 0) * pb[4] * pb[5] : 0;
+    return g;
+  };
 
   // Anchor slots (AMODE 1, 2): n_anc frames of the anchor grid h_a x w_a over
   // the extent (kh0_a, kh_l_a, kw0_a, kw_l_a), after the HR slots.  AMODE 1
@@ -241,23 +278,40 @@ void window_group_kernel(GroupArgs a) {
 
   V8 qf[KS];
   f32x16_t oacc[DT];
-  const int m = m0 + 32 * qhalf + c;
-  const bool qvalid = has_member && m < lq;
-  // Token of row r (0..31) of this wavefront's 32 queries, clamped into Q;
-  // row_ok: the row is one of the window's queries.
-  auto row_token = [&](int r) __attribute__((always_inline)) -> int {
-    const int mr = m0 + 32 * qhalf + r;
-    const int mm = (has_member && mr < lq) ? mr : 0;
-    const int qs = q_sp > 0 ? q_sp : 1, qw = qw_l > 0 ? qw_l : 1;
-    const int fr = fdiv(mm, qs, 1.0f / static_cast<float>(qs));
-    const int rr = mm - fr * q_sp;
-    const int hh = fdiv(rr, qw, 1.0f / static_cast<float>(qw));
-    const int ww = rr - hh * qw_l;
-    const int t = (q_t0 + fr) * L + (q_h0 + hh) * a.W + (q_w0 + ww);
-    return t < 0 ? 0 : (t >= a.q_tokens ? static_cast<int>(a.q_tokens) - 1 : t);
+  // Row r (0..31) of this wavefront's 32 queries: tile row 32*qhalf + r, which
+  // is query m0 + tile row of the window (PACK: of window A below pk_na rows,
+  // else query pk_qb0 + (tile row - pk_na) of window B).
+  auto in_b = [&](int r) __attribute__((always_inline)) -> bool {
+    return PACK && 32 * qhalf + r >= pk_na;
+  };
+  auto row_ok_g = [&](int r, const QGeo& gb) __attribute__((always_inline)) -> bool {
+    if (in_b(r)) return row1 >= 0 && pk_qb0 + 32 * qhalf + r - pk_na < gb.lq;
+    return has_member && m0 + 32 * qhalf + r < lq && (!PACK || 32 * qhalf + r < pk_na);
   };
   auto row_ok = [&](int r) __attribute__((always_inline)) -> bool {
-    return has_member && m0 + 32 * qhalf + r < lq;
+    if constexpr (PACK) return row_ok_g(r, b_geo());
+    return row_ok_g(r, QGeo{0, 0, 0, 1, 1, 0});
+  };
+  const bool qvalid = row_ok(c);
+  const int m = m0 + 32 * qhalf + c;  // this lane's query (the anchored forms)
+  // Token of row r, clamped into Q (gb: window B's geometry, PACK only).
+  auto row_token_g = [&](int r, const QGeo& gb) __attribute__((always_inline)) -> int {
+    const bool b = in_b(r);
+    const int mr = b ? pk_qb0 + 32 * qhalf + r - pk_na : m0 + 32 * qhalf + r;
+    const int mm = row_ok_g(r, gb) ? mr : 0;
+    const int hl = b ? gb.hl : qh_l, wl = b ? gb.wl : qw_l;
+    const int qs = hl * wl > 0 ? hl * wl : 1, qw = wl > 0 ? wl : 1;
+    const int fr = fdiv(mm, qs, 1.0f / static_cast<float>(qs));
+    const int rr = mm - fr * qs;
+    const int hh = fdiv(rr, qw, 1.0f / static_cast<float>(qw));
+    const int ww = rr - hh * qw;
+    const int t = ((b ? gb.t0 : q_t0) + fr) * L + ((b ? gb.h0 : q_h0) + hh) * a.W +
+                  ((b ? gb.w0 : q_w0) + ww);
+    return t < 0 ? 0 : (t >= a.q_tokens ? static_cast<int>(a.q_tokens) - 1 : t);
+  };
+  auto row_token = [&](int r) __attribute__((always_inline)) -> int {
+    if constexpr (PACK) return row_token_g(r, b_geo());
+    return row_token_g(r, QGeo{0, 0, 0, 1, 1, 0});
   };
   int qframe;  // this lane's query frame within the window
   // The anchored forms (AMODE 1, 2) sit at the register limit: they load Q
@@ -436,6 +490,26 @@ void window_group_kernel(GroupArgs a) {
   float lrun = 0.f;        // this lane's half of the row sum
   float mrun = 0.f;        // running max, valid once minit
   bool minit = false;      // wave-uniform: m has been set
+  // PACK, two windows: this lane's window's columns [mlo, mhi) of the 32-wide
+  // union, as a 32-bit set of the columns outside it.  S^T entry r holds key
+  // 8*(r/4) + 4*hf + r%4 of the step, i.e. that column; mask_cols sets the
+  // entries of outside columns to -inf after the S^T MFMAs of every step.
+  uint32_t colmask = 0;
+  if (PACK && row1 >= 0) {
+    const bool b = in_b(c);
+    const int mlo = (b ? p1[F + 10] : p0[F + 10]) - kw0;
+    const int mhi = mlo + (b ? p1[F + 11] : p0[F + 11]);
+    const uint32_t lo_bits = mlo <= 0 ? 0u : (mlo >= 32 ? ~0u : ((1u << mlo) - 1u));
+    const uint32_t hi_bits = mhi >= 32 ? 0u : (mhi <= 0 ? ~0u : ~((1u << mhi) - 1u));
+    colmask = lo_bits | hi_bits;
+  }
+  auto mask_cols = [&](f32x16_t& sc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = 8 * (r >> 2) + 4 * hf + (r & 3);
+      if ((colmask >> key) & 1u) sc[r] = -INFINITY;
+    }
+  };
   f32x16_t cneg = f32x16_t{};
   const typename E::h2 ones2 = {static_cast<T>(1.0f), static_cast<T>(1.0f)};
 
@@ -594,6 +668,7 @@ void window_group_kernel(GroupArgs a) {
     f32x16_t s_next;
     if (__builtin_expect(do_pv, 1)) {  // uniform
       if (__builtin_expect(s == nS_c - 1 && tail_valid < GKN, 0)) mask_tail(s_cur, tail_valid);
+      if (PACK && row1 >= 0) mask_cols(s_cur);  // uniform
       if (AMODE == 1 && __builtin_expect(fs >= P + nsh, 0)) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) s_cur[r] = admit ? s_cur[r] : -INFINITY;
@@ -732,12 +807,15 @@ void window_group_kernel(GroupArgs a) {
 __global__ void clear_amax_kernel(uint32_t* p) { *p = 0u; }
 
 template <typename T, int D>
-int launch_group(const GroupArgs& a, int members, int amode, uint32_t grid, hipStream_t stream) {
+int launch_group(const GroupArgs& a, int members, int amode, uint32_t grid, hipStream_t stream,
+                 bool pack = false) {
   if (a.amax_out) {
     hipLaunchKernelGGL(clear_amax_kernel, dim3(1), dim3(1), 0, stream, a.amax_out);
     SRDIT_LAUNCH_CHECK("clear_amax_kernel");
   }
-  if (amode == 1)
+  if (pack)
+    hipLaunchKernelGGL((window_group_kernel<T, D, 1, 0, true>), dim3(grid), dim3(128), 0, stream, a);
+  else if (amode == 1)
     hipLaunchKernelGGL((window_group_kernel<T, D, 1, 1>), dim3(grid), dim3(128), 0, stream, a);
   else if (amode == 2)
     hipLaunchKernelGGL((window_group_kernel<T, D, 1, 2>), dim3(grid), dim3(128), 0, stream, a);
@@ -759,7 +837,8 @@ int group_entry(const char* fn, const void* q, const void* k, const void* v, voi
                 const int32_t* params, const int32_t* groups, int n_w, int n_groups, int hr_base,
                 int H, int W, int64_t q_tokens, int64_t kv_tokens, int n_heads, int head_dim,
                 float scale, int ring_R, int ring_nc, const int32_t* ring_head,
-                uint32_t* amax_out, int members, int amode, int dtype, void* stream) {
+                uint32_t* amax_out, int members, int amode, int dtype, void* stream,
+                bool pack = false) {
   SRDIT_REQUIRE(q && k && v && o && params && groups, "%s: null pointer", fn);
   SRDIT_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
                 "%s: q/k/v/o must be 16-byte aligned", fn);
@@ -798,11 +877,13 @@ int group_entry(const char* fn, const void* q, const void* k, const void* v, voi
   SRDIT_REQUIRE(amode >= 0 && amode <= 2 && (amode == 0 || members == 1),
                 "%s: anchor mode %d (0 none, 1 per frame, 2 whole chunk) needs one member per "
                 "workgroup", fn, amode);
+  SRDIT_REQUIRE(!pack || (members == 1 && amode == 0),
+                "%s: packed tiles run one plain member per workgroup", fn);
   if (dtype == SRDIT_DTYPE_BF16)
-    return head_dim == 128 ? launch_group<__bf16, 128>(a, members, amode, grid, s)
-                           : launch_group<__bf16, 64>(a, members, amode, grid, s);
-  return head_dim == 128 ? launch_group<_Float16, 128>(a, members, amode, grid, s)
-                         : launch_group<_Float16, 64>(a, members, amode, grid, s);
+    return head_dim == 128 ? launch_group<__bf16, 128>(a, members, amode, grid, s, pack)
+                           : launch_group<__bf16, 64>(a, members, amode, grid, s, pack);
+  return head_dim == 128 ? launch_group<_Float16, 128>(a, members, amode, grid, s, pack)
+                         : launch_group<_Float16, 64>(a, members, amode, grid, s, pack);
 }
 
 }  // namespace
@@ -842,4 +923,28 @@ extern "C" int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, co
   return group_entry(fn, q, k, v, o, params, groups, n_w, n_groups, hr_base, H, W, q_tokens,
                      kv_tokens, n_heads, head_dim, scale, ring_frames, ring_cached, ring_head,
                      amax_out, members, anchor_mode, dtype, stream);
+}
+
+extern "C" int srdit_window_attn_packed_fwd(const void* q, const void* k, const void* v, void* o,
+                                            const int32_t* params, const int32_t* tiles,
+                                            int n_w, int n_tiles, int hr_base, int H, int W,
+                                            int64_t q_tokens, int64_t kv_tokens, int n_heads,
+                                            int head_dim, float scale, int ring_frames,
+                                            int ring_cached, const int32_t* ring_head,
+                                            uint32_t* amax_out, int dtype, void* stream) {
+  using namespace srdit;
+  const char* fn = "srdit_window_attn_packed_fwd";
+  if (ring_frames != 0) {
+    SRDIT_REQUIRE(ring_head != nullptr, "%s: null ring_head", fn);
+    SRDIT_REQUIRE(ring_frames >= 1 && ring_cached >= 0 && ring_cached <= ring_frames,
+                  "%s: need 0 <= ring_cached <= ring_frames (got %d, %d)", fn, ring_cached,
+                  ring_frames);
+    SRDIT_REQUIRE(hr_base >= 0 && static_cast<int64_t>(hr_base) +
+                      static_cast<int64_t>(ring_frames) * H * W <= kv_tokens,
+                  "%s: kv_tokens %lld do not cover the anchor prefix and %d ring frames", fn,
+                  static_cast<long long>(kv_tokens), ring_frames);
+  }
+  return group_entry(fn, q, k, v, o, params, tiles, n_w, n_tiles, hr_base, H, W, q_tokens,
+                     kv_tokens, n_heads, head_dim, scale, ring_frames, ring_cached, ring_head,
+                     amax_out, 1, 0, dtype, stream, true);
 }

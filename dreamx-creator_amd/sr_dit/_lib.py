@@ -36,6 +36,10 @@ SIGNATURES = {
                                                   _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64,
                                                   _c_int, _c_int, _c_f, _c_int, _c_int, _c_p,
                                                   _c_p, _c_int, _c_int, _c_int, _c_p]),
+    "srdit_window_attn_packed_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int,
+                                              _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64,
+                                              _c_int, _c_int, _c_f, _c_int, _c_int, _c_p,
+                                              _c_p, _c_int, _c_p]),
     "srdit_window_attn_shared_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64,
                                               _c_i64, _c_int, _c_int, _c_f, _c_int, _c_int, _c_p,
@@ -154,6 +158,23 @@ def window_attn_grouped_fwd(q, k, v, o, params, groups, *, n_w, n_groups, hr_bas
         _check(load().srdit_window_attn_grouped_fwd_ex(*args, *_ex_args(ring, amax_out),
                                                        int(members), int(anchor_mode), *tail),
                "srdit_window_attn_grouped_fwd_ex")
+
+
+def window_attn_packed_fwd(q, k, v, o, params, tiles, *, n_w, hr_base, H, W, n_heads, head_dim,
+                           kv_tokens, scale, ring=None, amax_out=None):
+    """The one-member window kernel over packed tiles (``blockgrid_hip.build_packed``:
+    int32 [T, 5], a tile holding the queries of one or two windows)."""
+    if q.dtype not in DTYPE_CODES:
+        raise ValueError(f"window attention needs bf16 or fp16, got {q.dtype}")
+    if (tiles.dim() != 2 or tiles.shape[1] != 5 or tiles.dtype != torch.int32
+            or not tiles.is_cuda or not tiles.is_contiguous()):
+        raise ValueError("window_attn_packed_fwd: tiles must be a contiguous device int32 [T, 5]")
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(params), _ptr(tiles),
+            int(n_w), int(tiles.shape[0]), int(hr_base), int(H), int(W), int(q.shape[0]),
+            int(kv_tokens), int(n_heads), int(head_dim), float(scale))
+    _check(load().srdit_window_attn_packed_fwd(*args, *_ex_args(ring, amax_out),
+                                               DTYPE_CODES[q.dtype], _stream(q.device)),
+           "srdit_window_attn_packed_fwd")
 
 
 QUANT_DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

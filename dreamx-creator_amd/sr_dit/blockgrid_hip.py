@@ -309,6 +309,121 @@ def build_singles(plan) -> torch.Tensor:
     return torch.tensor([rows[i] for i in order], dtype=torch.int32).reshape(-1, 4).contiguous()
 
 
+#: Width in tokens of the KV column union a two-window packed tile walks: one
+#: 32-key step is then one token row of the union, so a key's column is its
+#: index in the step and each lane's window mask is the same every step.
+PACK_WIDTH = 32
+
+
+def _packs(a, b) -> bool:
+    """Plain rows ``a`` then ``b`` (b to the right of a) can share packed tiles:
+    the same query frames and KV frames and rows, at most one 64-row tile of
+    queries each, and KV columns whose union is exactly PACK_WIDTH wide."""
+    if a[0:2] != b[0:2] or a[6:10] != b[6:10] or a[12] or b[12]:
+        return False
+    if not (0 < a[1] * a[4] * a[5] <= HIP_BLOCK_M and 0 < b[1] * b[4] * b[5] <= HIP_BLOCK_M):
+        return False
+    lo, hi = min(a[10], b[10]), max(a[10] + a[11], b[10] + b[11])
+    overlap = min(a[10] + a[11], b[10] + b[11]) - max(a[10], b[10])
+    return hi - lo == PACK_WIDTH and overlap >= 0 and b[10] > a[10]
+
+
+def build_packed(plan):
+    """Packed one-member tiles for a plain plan without an anchor prefix, or
+    None when no tile would hold two windows.
+
+    Windows whose KV cuboids differ only in their columns and whose column
+    union is PACK_WIDTH wide (horizontal neighbours of the shipped 4x4/r3
+    geometry: 28-column windows four columns apart) form runs.  A run's
+    queries, window after window, are cut into 64-row tiles, so a 48-query
+    window no longer pads a tile by 16 rows: a tile holds the end of one
+    window and the start of the next and walks the union of their columns,
+    each lane masking the columns outside its own window.  A run is packed
+    only when no tile would hold more than two windows.  Other windows get
+    one tile per 64 queries, as in ``build_singles``.
+
+    Returns int32 [T, 5]: (row A, first query of A, A's rows in the tile,
+    row B or -1, first query of B).  Launch order: query run by query run,
+    the heaviest tiles first within one (cost = tile rows' KV cuboid)."""
+    if not groups_supported(plan):
+        return None
+    p = plan["params"].tolist()
+    by_cuboid: dict = {}
+    for r, row in enumerate(p):
+        by_cuboid.setdefault((row[0], row[1], row[6], row[7], row[8], row[9]), []).append(r)
+    tiles, keys = [], []
+    packed_any = False
+
+    def add(tile, run_key, cost):
+        tiles.append(tile)
+        keys.append((run_key, -cost))
+
+    def singles(r):
+        row = p[r]
+        lq = _row_lq(plan, row)
+        cost = row[7] * row[9] * row[11]
+        for mt in range(-(-lq // HIP_BLOCK_M) if lq > 0 else 0):
+            add([r, HIP_BLOCK_M * mt, min(HIP_BLOCK_M, lq - HIP_BLOCK_M * mt), -1, 0], row[0], cost)
+
+    for rows in by_cuboid.values():
+        rows.sort(key=lambda r: (p[r][10], p[r][3]))
+        i = 0
+        while i < len(rows):
+            j = i
+            while j + 1 < len(rows) and _packs(p[rows[j]], p[rows[j + 1]]):
+                j += 1
+            run = rows[i:j + 1]
+            i = j + 1
+            if len(run) < 2:
+                singles(run[0])
+                continue
+            lqs = [_row_lq(plan, p[r]) for r in run]
+            offs = [0]
+            for lq in lqs:
+                offs.append(offs[-1] + lq)
+            cut = []
+            ok = True
+            for t0 in range(0, offs[-1], HIP_BLOCK_M):
+                t1 = min(t0 + HIP_BLOCK_M, offs[-1])
+                wins = [w for w in range(len(run)) if offs[w] < t1 and offs[w + 1] > t0]
+                if len(wins) > 2:
+                    ok = False
+                    break
+                cut.append((t0, t1, wins))
+            if not ok:
+                for r in run:
+                    singles(r)
+                continue
+            for t0, t1, wins in cut:
+                a = wins[0]
+                ra = run[a]
+                if len(wins) == 1:
+                    row = p[ra]
+                    add([ra, t0 - offs[a], t1 - t0, -1, 0], row[0], row[7] * row[9] * row[11])
+                else:
+                    rb = run[wins[1]]
+                    row = p[ra]
+                    packed_any = True
+                    add([ra, t0 - offs[a], offs[a + 1] - t0, rb, 0], row[0],
+                        row[7] * row[9] * PACK_WIDTH)
+    if not packed_any:
+        return None
+    order = sorted(range(len(tiles)), key=lambda i: keys[i])  # stable
+    return torch.tensor([tiles[i] for i in order], dtype=torch.int32).reshape(-1, 5).contiguous()
+
+
+def _packed_table(plan, device):
+    """build_packed's table on ``device`` (both cached in the plan), or None."""
+    if "packed_host" not in plan:
+        plan["packed_host"] = build_packed(plan)
+    if plan["packed_host"] is None:
+        return None
+    key = ("packed", device)
+    if key not in plan:
+        plan[key] = plan["packed_host"].to(device)
+    return plan[key]
+
+
 def shared_fraction(plan, groups: torch.Tensor) -> float:
     """Fraction of the members' KV frames that a pair fetches once for both
     (2 * shared frames / frames of both members, summed over the table): 1.0
@@ -422,9 +537,20 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     mode = 1 if anchor_mode == "frame" else 0
     if (plan["p_stride"] == P_FRAME) != (mode == 1):
         raise ValueError("run_blockgrid_hip: plan layout does not match anchor_mode.")
-    if kernel not in ("auto", "shared", "shared2", "grouped", "solo", "single"):
-        raise ValueError("run_blockgrid_hip: kernel must be auto, shared, shared2, grouped, solo "
-                         f"or single, got {kernel!r}")
+    if kernel not in ("auto", "shared", "shared2", "grouped", "solo", "single", "packed"):
+        raise ValueError("run_blockgrid_hip: kernel must be auto, shared, shared2, grouped, solo, "
+                         f"single or packed, got {kernel!r}")
+    if kernel == "packed":
+        tiles = _packed_table(plan, q.device) if anchor_mode is None else None
+        if tiles is None:
+            raise ValueError("run_blockgrid_hip: the plan has no windows to pack (plain rows "
+                             "without an anchor, at most 16 KV frames, neighbours whose KV "
+                             "column union is 32 tokens wide).")
+        _lib.window_attn_packed_fwd(
+            q, k_ext, v_ext, out, params, tiles, n_w=plan["n_w"], hr_base=hr_base, H=h, W=w,
+            n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0], scale=d ** -0.5, ring=ring,
+            amax_out=amax_out)
+        return out
     if kernel in ("auto", "shared", "shared2"):
         members = 2 if kernel == "shared2" else (SHARED_MEMBERS if kernel == "auto" else 4)
         share = (_share_tables(plan, h, w, d, q.device, members)
@@ -471,9 +597,14 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
         use_grouped = kernel == "grouped" or (plan["groups_paired_fraction"] >= 0.75 and
                                               plan["groups_shared_fraction"] >= 0.9 and
                                               plan["mean_kv_tokens"] >= GROUPED_MIN_KV)
+        # Otherwise one member per workgroup: packed tiles where two windows
+        # share one (48-query windows of 4x4 blocks), else one window per tile.
         if not use_grouped:
+            packs = kernel == "auto" and anchor_mode is None and \
+                _packed_table(plan, q.device) is not None
             return run_blockgrid_hip(q, k_ext, v_ext, out, plan=plan, f_cur=f_cur, h=h, w=w, n=n,
-                                     d=d, anchor_mode=anchor_mode, kernel="solo", ring=ring,
+                                     d=d, anchor_mode=anchor_mode,
+                                     kernel="packed" if packs else "solo", ring=ring,
                                      hr_base=hr_base, amax_out=amax_out)
     if use_grouped:
         _lib.window_attn_grouped_fwd(

@@ -129,6 +129,35 @@ int srdit_window_attn_grouped_fwd_ex(const void* q, const void* k, const void* v
                                      void* stream);
 
 /*
+ * Block-grid window attention, forward, plain windows without an anchor prefix,
+ * one workgroup per 64-row tile, where a tile may hold the queries of two
+ * windows (the end of one, the start of the next).
+ *
+ * Replaces the same launch as srdit_window_attn_fwd mode 0
+ * (run_blockgrid_triton -> _blockgrid_fused_kernel, blockgrid_triton.py:392-422,
+ * :184-278) for tables whose rows all have a_frames == 0 and at most 16 KV
+ * frames.  Windows of fewer than 64 queries (48 for 4x4-token blocks over three
+ * frames) otherwise pad their tile; two of them share one here.
+ *
+ * tiles       int32 [n_tiles, 5] device table: row A, A's first query, A's rows
+ *             in the tile (1..64), row B or -1, B's first query.  Tile row r is
+ *             query (first + r) of A for r below A's rows, else query
+ *             (B's first + r - A's rows) of B; rows past a window's queries are
+ *             not written.  A and B must have the same query frames and the
+ *             same KV frames and token rows, and their KV column ranges must
+ *             span exactly 32 columns together: the tile walks that union and
+ *             each query drops the columns outside its own window.
+ * Other arguments as srdit_window_attn_grouped_fwd_ex (members 1, anchor_mode 0).
+ */
+int srdit_window_attn_packed_fwd(const void* q, const void* k, const void* v, void* o,
+                                 const int32_t* params, const int32_t* tiles,
+                                 int n_w, int n_tiles, int hr_base, int H, int W,
+                                 int64_t q_tokens, int64_t kv_tokens, int n_heads,
+                                 int head_dim, float scale, int ring_frames, int ring_cached,
+                                 const int32_t* ring_head, uint32_t* amax_out, int dtype,
+                                 void* stream);
+
+/*
  * Block-grid window attention, forward, with K/V fetches shared between
  * neighbouring windows: up to `members` (2 or 4) 64-query members per
  * workgroup of 2*members wavefronts walk a host-built step schedule, and each
