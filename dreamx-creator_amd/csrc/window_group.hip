@@ -217,13 +217,17 @@ void window_group_kernel(GroupArgs a) {
   struct QGeo {
     int t0, h0, w0, hl, wl, lq;
   };
+  // One read per call site group (the prologue, the epilogue), none for a
+  // tile of one window.
   auto b_geo = [&]() __attribute__((always_inline)) -> QGeo {
-    const int32_t* pb = p1;
-    asm volatile("" : "+s"(pb));
-    QGeo g;
-    g.t0 = pb[0]; g.h0 = pb[2]; g.w0 = pb[3];
-    g.hl = max(pb[4], 1); g.wl = max(pb[5], 1);
-    g.lq = (PACK && row1 >= 0) ? max(pb[1], 0) * pb[4] * pb[5] : 0;
+    QGeo g{0, 0, 0, 1, 1, 0};
+    if (PACK && row1 >= 0) {  // uniform
+      const int32_t* pb = p1;
+      asm volatile("" : "+s"(pb));
+      g.t0 = pb[0]; g.h0 = pb[2]; g.w0 = pb[3];
+      g.hl = max(pb[4], 1); g.wl = max(pb[5], 1);
+      g.lq = max(pb[1], 0) * pb[4] * pb[5];
+    }
     return g;
   };
 
@@ -603,10 +607,11 @@ void window_group_kernel(GroupArgs a) {
                                             (static_cast<uint32_t>(tok_bytes) << 16)),
                            static_cast<int>(a.q_tokens), 0x00020000};
     const int pos = lane % CPKQ, sub_q = (lane & 15) / LPKQ;
+    const QGeo gb = b_geo();
     static_for<NL>([&](auto qc) __attribute__((always_inline)) {
       constexpr int qi = decltype(qc)::value;
       const int r = qi * KPIQ + (lane >> 4) * (16 / LPKQ) + sub_q;
-      dma_x4(qrsrc, qreg + qi * 1024, row_token(r), (pos ^ swz_k<D>(r)) * 16);
+      dma_x4(qrsrc, qreg + qi * 1024, row_token_g(r, gb), (pos ^ swz_k<D>(r)) * 16);
     });
   }
   if (nsteps > 0) fill_next(0);
@@ -790,12 +795,13 @@ void window_group_kernel(GroupArgs a) {
   compiler_fence();
   {
     const int pos = lane % CPKQ, sub_q = (lane & 15) / LPKQ;
+    const QGeo gb = b_geo();
 #pragma unroll
     for (int qi = 0; qi < NL; ++qi) {
       const int r = qi * KPIQ + (lane >> 4) * (16 / LPKQ) + sub_q;
       const i32x4_t v = *reinterpret_cast<const i32x4_t*>(ob + (r * CPKQ + (pos ^ swz_k<D>(r))) * 16);
-      if (row_ok(r)) {
-        T* op = reinterpret_cast<T*>(a.o) + head * D + static_cast<int64_t>(row_token(r)) * tok +
+      if (row_ok_g(r, gb)) {
+        T* op = reinterpret_cast<T*>(a.o) + head * D + static_cast<int64_t>(row_token_g(r, gb)) * tok +
                 pos * 8;
         *reinterpret_cast<i32x4_t*>(op) = v;
       }

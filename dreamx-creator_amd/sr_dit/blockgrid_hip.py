@@ -335,12 +335,13 @@ def build_packed(plan):
     Windows whose KV cuboids differ only in their columns and whose column
     union is PACK_WIDTH wide (horizontal neighbours of the shipped 4x4/r3
     geometry: 28-column windows four columns apart) form runs.  A run's
-    queries, window after window, are cut into 64-row tiles, so a 48-query
-    window no longer pads a tile by 16 rows: a tile holds the end of one
-    window and the start of the next and walks the union of their columns,
-    each lane masking the columns outside its own window.  A run is packed
-    only when no tile would hold more than two windows.  Other windows get
-    one tile per 64 queries, as in ``build_singles``.
+    queries, window after window, are cut into tiles of at most 64 rows, so a
+    48-query window no longer pads a tile by 16 rows: a tile holds the end of
+    one window and the start of the next and walks the union of their columns,
+    each lane masking the columns outside its own window.  The cut is greedy
+    and never puts a third window in a tile (40-query windows: three windows in
+    two tiles).  Other windows get one tile per 64 queries, as in
+    ``build_singles``.
 
     Returns int32 [T, 5]: (row A, first query of A, A's rows in the tile,
     row B or -1, first query of B).  Launch order: query run by query run,
@@ -377,39 +378,48 @@ def build_packed(plan):
             if len(run) < 2:
                 singles(run[0])
                 continue
+            # Greedy cut: a tile takes what is left of window A and, when that is
+            # under 64 rows, the head of the next window B; never a third one.
             lqs = [_row_lq(plan, p[r]) for r in run]
-            offs = [0]
-            for lq in lqs:
-                offs.append(offs[-1] + lq)
-            cut = []
-            ok = True
-            for t0 in range(0, offs[-1], HIP_BLOCK_M):
-                t1 = min(t0 + HIP_BLOCK_M, offs[-1])
-                wins = [w for w in range(len(run)) if offs[w] < t1 and offs[w + 1] > t0]
-                if len(wins) > 2:
-                    ok = False
-                    break
-                cut.append((t0, t1, wins))
-            if not ok:
-                for r in run:
-                    singles(r)
-                continue
-            for t0, t1, wins in cut:
-                a = wins[0]
-                ra = run[a]
-                if len(wins) == 1:
-                    row = p[ra]
-                    add([ra, t0 - offs[a], t1 - t0, -1, 0], row[0], row[7] * row[9] * row[11])
-                else:
-                    rb = run[wins[1]]
-                    row = p[ra]
-                    packed_any = True
-                    add([ra, t0 - offs[a], offs[a + 1] - t0, rb, 0], row[0],
-                        row[7] * row[9] * PACK_WIDTH)
+            wi, pos = 0, 0
+            while wi < len(run):
+                ra = run[wi]
+                row = p[ra]
+                na = min(HIP_BLOCK_M, lqs[wi] - pos)
+                if na == HIP_BLOCK_M or wi + 1 == len(run):
+                    add([ra, pos, na, -1, 0], row[0], row[7] * row[9] * row[11])
+                    pos += na
+                    if pos >= lqs[wi]:
+                        wi, pos = wi + 1, 0
+                    continue
+                nb = min(HIP_BLOCK_M - na, lqs[wi + 1])
+                packed_any = True
+                add([ra, pos, na, run[wi + 1], 0], row[0], row[7] * row[9] * PACK_WIDTH)
+                wi, pos = (wi + 2, 0) if nb == lqs[wi + 1] else (wi + 1, nb)
     if not packed_any:
         return None
     order = sorted(range(len(tiles)), key=lambda i: keys[i])  # stable
     return torch.tensor([tiles[i] for i in order], dtype=torch.int32).reshape(-1, 5).contiguous()
+
+
+#: ``kernel="auto"`` runs packed tiles when they remove at least this fraction
+#: of the one-window tiles.  The packed form costs more per tile than the
+#: one-window form (A/B, one process: c3, 3% fewer tiles, 423 against 391 us;
+#: c2, 5% fewer, 238 against 225 us), and wins where the tiles drop by a sixth
+#: (the shipped 4x4/r3 geometry: 200 against 240 tiles, 1260 against 1367 us).
+PACKED_MIN_SAVING = 0.10
+
+
+def packed_saving(plan) -> float:
+    """Fraction of build_singles' tiles that build_packed removes (0 when the plan
+    does not pack); cached in the plan."""
+    if "packed_saving" not in plan:
+        if "packed_host" not in plan:
+            plan["packed_host"] = build_packed(plan)
+        host = plan["packed_host"]
+        plan["packed_saving"] = 0.0 if host is None else \
+            1.0 - host.shape[0] / max(1, build_singles(plan).shape[0])
+    return plan["packed_saving"]
 
 
 def _packed_table(plan, device):
@@ -601,7 +611,7 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
         # share one (48-query windows of 4x4 blocks), else one window per tile.
         if not use_grouped:
             packs = kernel == "auto" and anchor_mode is None and \
-                _packed_table(plan, q.device) is not None
+                packed_saving(plan) >= PACKED_MIN_SAVING
             return run_blockgrid_hip(q, k_ext, v_ext, out, plan=plan, f_cur=f_cur, h=h, w=w, n=n,
                                      d=d, anchor_mode=anchor_mode,
                                      kernel="packed" if packs else "solo", ring=ring,

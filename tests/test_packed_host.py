@@ -103,13 +103,34 @@ def test_no_tile_holds_more_than_two_windows_and_work_drops():
     assert work_packed < 0.95 * work_singles
 
 
-def test_plans_that_do_not_pack():
-    # 8x8 blocks of radius 1 (the c3 geometry): 64-query windows fill their tiles
+def test_greedy_cut_packs_40_query_windows():
+    # c3: 8x8 blocks of radius 1; the ragged last block row has 40-query windows
+    # whose interior neighbours span 32 columns: three windows in two tiles
     from sr_dit import workloads as wl
     plan = bgh.build_plan(wl.window_spec("c3"))
-    assert bgh.build_packed(plan) is None
+    tiles = bgh.build_packed(plan)
+    p = plan["params"].tolist()
+    pairs = [t for t in tiles.tolist() if t[3] >= 0]
+    assert pairs and all(p[a][1] * p[a][4] * p[a][5] == 40 for a, *_ in pairs)
+    assert tiles.shape[0] < bgh.build_singles(plan).shape[0]
+
+
+def test_plans_that_do_not_pack():
+    # c1: 16x16 frames of 8x8 blocks, every window spans the same 16 columns
+    from sr_dit import workloads as wl
+    assert bgh.build_packed(bgh.build_plan(wl.window_spec("c1"))) is None
     # a 28-token-wide frame: every window spans all 28 columns, no union is 32 wide
     assert bgh.build_packed(bgh.build_plan(_shipped(h=16, w=28))) is None
     # an anchored plan is never packed
     spec = _shipped()
     assert bgh.build_packed(bgh.build_plan(spec, anchor_mode="frame")) is None
+
+
+def test_auto_packs_only_where_tiles_drop():
+    """kernel="auto" takes packed tiles only when they remove PACKED_MIN_SAVING of
+    the one-window tiles: the shipped geometry at every cache length, not c1-c4."""
+    from sr_dit import workloads as wl
+    for f_kv in (3, 6, 9, 12):
+        assert bgh.packed_saving(bgh.build_plan(_shipped(f_kv=f_kv))) >= bgh.PACKED_MIN_SAVING
+    for cfg in ("c1", "c2", "c3", "c4"):
+        assert bgh.packed_saving(bgh.build_plan(wl.window_spec(cfg))) < bgh.PACKED_MIN_SAVING
