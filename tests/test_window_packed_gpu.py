@@ -51,7 +51,7 @@ def _launch(spec, q, k, v, kernel, **kw):
 SMALL = [
     ("3of6_24x40", _spec(3, 6, 24, 40)),
     ("3of3_20x36", _spec(3, 3, 20, 36)),
-    ("3of9_16x44_ragged", _spec(3, 9, 17, 44)),
+    ("3of9_17x44_ragged", _spec(3, 9, 17, 44)),
     ("3of12_21x52", _spec(3, 12, 21, 52)),
 ]
 
