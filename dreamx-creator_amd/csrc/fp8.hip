@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const T* __restrict__
 // ---------------------------------------------------------------------- GEMM
 
 constexpr int GT = 256;                       // tile rows (M) and columns (N)
-constexpr int G_GROUP_M = 8;                  // M tiles per raster group
+constexpr int G_GROUP_M = 4;                  // M tiles per raster group
 
 struct GemmArgs {
   const uint8_t* a;      // [M, K]
@@ -201,12 +201,10 @@ struct GemmArgs {
   uint32_t* amax_out;  // AMAX epilogue only
 };
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
 __device__ __forceinline__ void compiler_fence_gemm() { asm volatile("" ::: "memory"); }
 
 // Wait until at most N vector-memory operations of this wavefront are in
-// flight (its newest fills), and for all its LDS reads.
+// flight (its newest ones), and for all its LDS reads (lgkmcnt(0)).
 template <int N>
 __device__ __forceinline__ void waitcnt_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt out of range");
@@ -366,151 +364,138 @@ __global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_quant_kernel(
   }
 }
 
-// The epilogue of one wavefront's NI x NJ blocks of 32 x 32: acc[i][j] is
-// out^T[n-subtile i][m-subtile j] (the weight is the MFMA A operand); lane l
-// holds row m = m_base + 32 j + (l & 31) and columns n = n_base + 32 i + 8 (r/4)
-// + 4 (l/32) + r%4, stored as 8-byte runs of four bf16.
-// EPI 0: out = bf16(v); EPI 1: out = bf16(gelu(bf16(v))), the Linear's bf16
-// output fed to nn.GELU(approximate='tanh').  AMAX: also the max |out| (float
-// bits) of the whole output into *g.amax_out, for a per-tensor quantiser.
-template <int EPI, bool AMAX, int NI, int NJ>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16_t (&acc)[NI][NJ],
-                                              int m_base, int n_base, int lane) {
-  const int mrow = lane & 31;
-  const int ncol = 4 * (lane >> 5);
-  uint32_t amax = 0;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int m = m_base + j * 32 + mrow;
-    if (m >= g.M) continue;
-    const float sa = g.sa[g.sa_per_row ? m : 0];
-    uint16_t* orow = g.out + (int64_t)m * g.ldo;
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n_base + i * 32 + 8 * q + ncol;
-        if (n >= g.N) continue;
-        float sb[4], bias[4];
-        if (g.sb_per_col) {
-          const float4 v = *reinterpret_cast<const float4*>(g.sb + n);
-          sb[0] = v.x; sb[1] = v.y; sb[2] = v.z; sb[3] = v.w;
-        } else {
-          sb[0] = sb[1] = sb[2] = sb[3] = g.sb[0];
-        }
-        if (g.bias) {
-          const uint2 bv = *reinterpret_cast<const uint2*>(g.bias + n);
-          bias[0] = __uint_as_float(bv.x << 16);
-          bias[1] = __uint_as_float(bv.x & 0xffff0000u);
-          bias[2] = __uint_as_float(bv.y << 16);
-          bias[3] = __uint_as_float(bv.y & 0xffff0000u);
-        } else {
-          bias[0] = bias[1] = bias[2] = bias[3] = 0.f;
-        }
-        float v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * q + r] * sa * sb[r] + bias[r];
-        typedef float f32x2v __attribute__((ext_vector_type(2)));
-        typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-        bf16x2v p0 = __builtin_convertvector(f32x2v{v[0], v[1]}, bf16x2v);
-        bf16x2v p1 = __builtin_convertvector(f32x2v{v[2], v[3]}, bf16x2v);
-        if (EPI == 1) {
-          const uint32_t b0 = __builtin_bit_cast(uint32_t, p0), b1 = __builtin_bit_cast(uint32_t, p1);
-          const float r0 = __uint_as_float(b0 << 16), r1 = __uint_as_float(b0 & 0xffff0000u);
-          const float r2 = __uint_as_float(b1 << 16), r3 = __uint_as_float(b1 & 0xffff0000u);
-          p0 = __builtin_convertvector(f32x2v{gelu_tanh(r0), gelu_tanh(r1)}, bf16x2v);
-          p1 = __builtin_convertvector(f32x2v{gelu_tanh(r2), gelu_tanh(r3)}, bf16x2v);
-        }
-        uint2 packed;
-        packed.x = __builtin_bit_cast(uint32_t, p0);
-        packed.y = __builtin_bit_cast(uint32_t, p1);
-        if (AMAX) {
-          amax = max(amax, max((packed.x & 0x7fffu) << 16, packed.x & 0x7fff0000u));
-          amax = max(amax, max((packed.y & 0x7fffu) << 16, packed.y & 0x7fff0000u));
-        }
-        *reinterpret_cast<uint2*>(orow + n) = packed;
-      }
-    }
-  }
-  if (AMAX) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, o));
-    if (lane == 0) raise_max_word(g.amax_out, amax);
-  }
-}
+// ------------------------------------------------------------------ the GEMM
+//
+// One persistent workgroup of eight wavefronts per CU.  Workgroup b runs on
+// XCD b % 8; each XCD owns one contiguous range of 256 x 256 output tiles
+// (rastered in groups of G_GROUP_M tile rows, column by column, so the
+// workgroups of one XCD share operand rows in its L2), and workgroup slot
+// b / 8 walks that range with a stride of the XCD's workgroup count.
+//
+// Operands reach LDS by buffer_load_dwordx4 ... lds, one 128-byte K stage of
+// both 256-row tiles at a time (whole 128-byte lines: the L2 -> LDS path is
+// limited by lines, not bytes) through two 64 KB slots.  Each stage is computed
+// as two 64-byte sub-steps of v_mfma_f32_32x32x64_f8f6f4 with double-buffered
+// fragments: the MFMAs of one sub-step run while the fragments of the next are
+// read, so the only barrier is once per stage, where the stage after next is
+// filled into the slot the current stage has just left (its fragments are in
+// registers by then).  The K loop is one stream of stages across tile
+// boundaries, so the next tile's first stages are in flight while a tile
+// finishes.  Wave (wm, wn) = (w & 1, w >> 1) owns activation rows
+// [128 wm, +128) and weight rows [64 wn, +64): 2 x 4 blocks, 128 accumulators,
+// which hold out^T (the weight is the MFMA's A operand).
+//
+// vmcnt is counted exactly, since the fills are inline asm the compiler cannot
+// see: each wavefront issues 8 fill DMAs per stage, one epilogue-data DMA per
+// tile (wavefronts 0-2, just before the tile's last stage), and EPI_STORES
+// stores per tile; at the barrier before stage S + 1 is read, only the stores
+// of a tile that ended right before stage S can be newer than fill S + 1.
+//
+// Epilogue data (per-row activation scales, per-column weight scales, bias)
+// is DMA'd into one of three 3 KB LDS regions per tile, so no epilogue load
+// touches vmcnt.  Each 32 x 32 output block is transposed through a 2 KB
+// per-wavefront LDS buffer and stored as 16 rows x 64 bytes per instruction;
+// rows past M and columns past N fall outside the store descriptor.
+//
+// Measured on one MI355X (per-tensor scales, bias, same box): 21600 x 3072 x
+// 3072 in 169-175 us (2.35-2.43 PFLOP/s), 21600 x 14336 x 3072 in 805-815 us
+// (2.33-2.36), 21600 x 3072 x 14336 in 760-790 us (2.41-2.50); without its
+// fills the same loop runs 2.85-3.3 PFLOP/s, where core-clock counters show the
+// MFMA pipe ~99% busy at the ~1.57 GHz the chip sustains under that load.
+constexpr int G_FK = 128;                      // K bytes per fill stage
+constexpr int G_OPB = GT * G_FK;               // one operand tile of a stage: 32 KB
+constexpr int G_SLOT = 2 * G_OPB;              // 64 KB
+constexpr int G_NI = 2, G_NJ = 4;              // 32 x 32 blocks per wavefront (weight, act)
+constexpr int EPI_STORES = G_NI * G_NJ * 2;    // epilogue stores per wavefront per tile
+constexpr int G_EPI_OFF = 2 * G_SLOT;          // three epilogue-data regions
+constexpr int G_EPI_REG = 3 * 1024;            // sa[256] f32, sb[256] f32, bias[256] bf16 (+pad)
+constexpr int G_STG_OFF = G_EPI_OFF + 3 * G_EPI_REG;
+constexpr int G_LDS = G_STG_OFF + 8 * 2048;    // + 2 KB transpose buffer per wavefront
 
-// The fp8 GEMM: a 256 x 256 output tile per workgroup of eight wavefronts
-// (two per SIMD); wavefront (wm, wn) = (w & 1, w >> 1) owns activation rows
-// [128 wm, +128) and weight rows [64 wn, +64), 2 x 4 blocks of
-// v_mfma_f32_32x32x64_f8f6f4 (128 accumulator registers).  K advances 128
-// bytes per stage (whole 128-byte lines per fill row) through a two-stage
-// 2 x 64 KB LDS ring filled one stage ahead by buffer_load ... lds; each stage
-// runs two 64-byte MFMA depths.  LDS rows are 128 bytes; chunk c of row r
-// sits at c ^ ((r >> 1) & 7), so the fragment reads of 16 lanes cover all 64
-// banks.  Measured against alternatives on one MI355X (21600 x 3072 x 3072,
-// per-tensor scales): 64-byte stages in a four-stage ring filled three or
-// four ahead, 4 wavefronts of 128 x 128, register-staged fills and
-// double-buffered fragments were all equal or slower (1.43-1.80 PFLOP/s
-// against 1.79-1.87); without its fills this kernel runs 2.56 PFLOP/s, so the
-// L2 -> LDS fills, not the MFMA issue, bound it.
-constexpr int QK = 128;
-constexpr int Q_OPB = GT * QK;             // 32 KB per operand per stage
-constexpr int Q_STAGE = 2 * Q_OPB;
+struct GemmFrags {
+  i32x8_t w[G_NI], x[G_NJ];
+};
 
 template <int EPI, bool AMAX>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void fp8_gemm_wide_kernel(const GemmArgs g) {
-  constexpr int NI = 2, NJ = 4;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * Q_STAGE];
-
+void fp8_gemm_kernel(const GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[G_LDS];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave & 1, wn = wave >> 1;
 
   const uint32_t n_tasks = (uint32_t)g.tiles_m * g.tiles_n;
-  const uint32_t task = xcd_task(blockIdx.x, n_tasks);
+  const uint32_t xcd = blockIdx.x & 7u, wslot = blockIdx.x >> 3, per = gridDim.x >> 3;
+  const uint32_t r0 = xcd * (n_tasks >> 3) + min(xcd, n_tasks & 7u);
+  const uint32_t r1 = r0 + (n_tasks >> 3) + (xcd < (n_tasks & 7u) ? 1u : 0u);
+  const int my_tiles = (r0 + wslot < r1) ? (int)((r1 - r0 - wslot + per - 1) / per) : 0;
+  if (my_tiles == 0) return;
+  const int nks = g.K / G_FK;  // stages per tile
+  const int n_total = my_tiles * nks;
   const int width = G_GROUP_M * g.tiles_n;
-  const int group = task / width;
-  const int first_m = group * G_GROUP_M;
-  const int gsize = min(g.tiles_m - first_m, G_GROUP_M);
-  const int tm = first_m + (int)(task % width) % gsize;
-  const int tn = (int)(task % width) / gsize;
-  const int m0 = tm * GT, n0 = tn * GT;
-
-  auto rsrc_of = [](const uint8_t* p, int64_t bytes) __attribute__((always_inline)) -> i32x4_t {
+  auto coords = [&](int t, int& m0, int& n0) __attribute__((always_inline)) {
+    const uint32_t task = r0 + wslot + per * (uint32_t)t;
+    const int group = task / width;
+    const int first_m = group * G_GROUP_M;
+    const int gsize = min(g.tiles_m - first_m, G_GROUP_M);
+    m0 = (first_m + (int)(task % width) % gsize) * GT;
+    n0 = ((int)(task % width) / gsize) * GT;
+  };
+  auto rsrc_of = [](const void* p, int64_t bytes) __attribute__((always_inline)) -> i32x4_t {
     const uint64_t a = reinterpret_cast<uint64_t>(p);
     return i32x4_t{static_cast<int>(static_cast<uint32_t>(a)),
                    static_cast<int>(static_cast<uint32_t>(a >> 32)), static_cast<int>(bytes),
                    0x00020000};
   };
-  const i32x4_t rs_a = rsrc_of(g.a + (int64_t)m0 * g.K, (int64_t)(g.M - m0) * g.K);
-  const i32x4_t rs_b = rsrc_of(g.b + (int64_t)n0 * g.K, (int64_t)(g.N - n0) * g.K);
 
-  // Fill: wavefront w writes rows [32 w, +32) of both tiles in four 1 KB loads
-  // (8 rows of 128 bytes); lane l -> row 8 q + l/8, position l%8, holding
-  // source chunk (l%8) ^ ((row >> 1) & 7) = (l%8) ^ ((4 (q & 1) + (l >> 4)) & 7).
+  // Fill: wavefront w writes rows [32 w, +32) of both tiles in four 1 KB DMAs
+  // each (8 rows of 128 bytes); lane l -> row 8 q + l/8, position l%8 holding
+  // source chunk (l%8) ^ ((row >> 1) & 7).  Rows past M or N read as zero
+  // through the descriptor's range check.
   const int fpos = lane & 7;
   const int fbase = (wave * 32 + (lane >> 3)) * g.K;
   const int fv_even = fbase + ((fpos ^ ((lane >> 4) & 7)) * 16);
   const int fv_odd = fbase + ((fpos ^ ((4 + (lane >> 4)) & 7)) * 16);
   const int frow8 = 8 * g.K;
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * 32 * QK;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  const uint32_t lds_w = lds_base + wave * 32 * G_FK;
   auto dma = [](i32x4_t rsrc, int voff, int soff, uint32_t lds) __attribute__((always_inline)) {
     asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
                  "{m0}"(lds)
                  : "memory");
   };
-  auto fill = [&](int stage, int kt) __attribute__((always_inline)) {
-    const uint32_t base = lds0 + stage * Q_STAGE;
-    const int koff = kt * QK;
+  int f_t = 0, f_kt = 0, f_slot = 0;  // fill cursor: tile, stage in tile, slot
+  i32x4_t f_ra = {}, f_rb = {};
+  auto fill_next = [&]() __attribute__((always_inline)) {
+    int m0, n0;
+    coords(f_t, m0, n0);
+    if (f_kt == nks - 1 && wave < 3) {  // the tile's epilogue data, ahead of its last stage
+      i32x4_t r;
+      if (wave == 0) r = rsrc_of(g.sa + m0, g.sa_per_row ? (int64_t)(g.M - m0) * 4 : 0);
+      else if (wave == 1) r = rsrc_of(g.sb + n0, g.sb_per_col ? (int64_t)(g.N - n0) * 4 : 0);
+      else r = rsrc_of(g.bias ? (const void*)(g.bias + n0) : (const void*)g.b,
+                       g.bias ? (int64_t)(g.N - n0) * 2 : 0);
+      dma(r, 16 * lane, 0, lds_base + G_EPI_OFF + (f_t % 3) * G_EPI_REG + wave * 1024);
+    }
+    if (f_kt == 0) {
+      f_ra = rsrc_of(g.a + (int64_t)m0 * g.K, (int64_t)(g.M - m0) * g.K);
+      f_rb = rsrc_of(g.b + (int64_t)n0 * g.K, (int64_t)(g.N - n0) * g.K);
+    }
+    const uint32_t base = lds_w + f_slot * G_SLOT;
+    const int koff = f_kt * G_FK;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      dma(rs_a, ((q & 1) ? fv_odd : fv_even) + q * frow8, koff, base + q * 1024);
+      dma(f_ra, ((q & 1) ? fv_odd : fv_even) + q * frow8, koff, base + q * 1024);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      dma(rs_b, ((q & 1) ? fv_odd : fv_even) + q * frow8, koff, base + Q_OPB + q * 1024);
+      dma(f_rb, ((q & 1) ? fv_odd : fv_even) + q * frow8, koff, base + G_OPB + q * 1024);
+    if (++f_kt == nks) { f_kt = 0; ++f_t; }
+    f_slot ^= 1;
   };
 
+  // Fragment reads: lane l reads row l & 31, bytes [64 kk + 32 (l >> 5), +32)
+  // of the stage: two 16-byte chunks at their swizzled positions, which makes
+  // the reads of 16 lanes cover all 64 banks.
   const int rrow = lane & 31;
   const int rswz = (rrow >> 1) & 7;
   const int h2 = 2 * (lane >> 5);
@@ -518,51 +503,173 @@ void fp8_gemm_wide_kernel(const GemmArgs g) {
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) roff[kk][h] = rrow * QK + (((kk * 4 + h2 + h) ^ rswz) * 16);
+    for (int h = 0; h < 2; ++h) roff[kk][h] = rrow * G_FK + (((kk * 4 + h2 + h) ^ rswz) * 16);
 
-  f32x16_t acc[NI][NJ];
+  f32x16_t acc[G_NI][G_NJ];
 #pragma unroll
-  for (int i = 0; i < NI; ++i)
+  for (int i = 0; i < G_NI; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16_t{};
-  struct Frags {
-    i32x8_t w[NI], x[NJ];
+    for (int j = 0; j < G_NJ; ++j) acc[i][j] = f32x16_t{};
+  auto mma_j = [&](const GemmFrags& f, int j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < G_NI; ++i)
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[i], f.x[j], acc[i][j], 0,
+                                                                  0, 0, 0, 0, 0);
   };
-  auto read_sub = [&](int st, auto kk_c) __attribute__((always_inline)) -> Frags {
+  // The MFMAs of fc, with the reads of sub-step kk of `slot` into fn between
+  // them (the scheduling barriers keep that order).
+  auto compute = [&](const GemmFrags& fc, GemmFrags& fn, int slot, auto kk_c)
+                     __attribute__((always_inline)) {
     constexpr int kk = decltype(kk_c)::value;
-    const uint8_t* ta = smem + st * Q_STAGE + wm * 128 * QK;
-    const uint8_t* tb = smem + st * Q_STAGE + Q_OPB + wn * 64 * QK;
-    Frags f;
+    const uint8_t* ta = smem + slot * G_SLOT + wm * 128 * G_FK;
+    const uint8_t* tb = smem + slot * G_SLOT + G_OPB + wn * 64 * G_FK;
+    mma_j(fc, 0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) f.w[i] = read_frag(tb + i * 32 * QK, roff[kk][0], roff[kk][1]);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) f.x[j] = read_frag(ta + j * 32 * QK, roff[kk][0], roff[kk][1]);
-    return f;
-  };
-  auto mma = [&](const Frags& f) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int i = 0; i < NI; ++i)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[i], f.x[j], acc[i][j], 0,
-                                                                    0, 0, 0, 0, 0);
+    for (int i = 0; i < G_NI; ++i) fn.w[i] = read_frag(tb + i * 32 * G_FK, roff[kk][0], roff[kk][1]);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_j(fc, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    fn.x[0] = read_frag(ta + 0 * 32 * G_FK, roff[kk][0], roff[kk][1]);
+    fn.x[1] = read_frag(ta + 1 * 32 * G_FK, roff[kk][0], roff[kk][1]);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_j(fc, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    fn.x[2] = read_frag(ta + 2 * 32 * G_FK, roff[kk][0], roff[kk][1]);
+    fn.x[3] = read_frag(ta + 3 * 32 * G_FK, roff[kk][0], roff[kk][1]);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_j(fc, 3);
   };
 
-  const int nk = g.K / QK;
-  fill(0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    compiler_fence_gemm();
-    waitcnt_vm<0>();
-    __builtin_amdgcn_s_barrier();
-    compiler_fence_gemm();
-    const int st = kt & 1;
-    if (kt + 1 < nk) fill(st ^ 1, kt + 1);
-    const Frags f0 = read_sub(st, std::integral_constant<int, 0>{});
-    const Frags f1 = read_sub(st, std::integral_constant<int, 1>{});
-    mma(f0);
-    mma(f1);
+  // Prologue: stages 0 and 1 in flight; wait for stage 0.
+  fill_next();
+  int pro_newer = 0;
+  if (n_total > 1) {
+    pro_newer = 8 + ((nks <= 2 && wave < 3) ? 1 : 0);  // stage 1 (and its tile's epilogue data)
+    fill_next();
   }
-  gemm_epilogue<EPI, AMAX, NI, NJ>(g, acc, m0 + wm * 128, n0 + wn * 64, lane);
+  compiler_fence_gemm();
+  if (pro_newer == 0) waitcnt_vm<0>();
+  else if (pro_newer == 8) waitcnt_vm<8>();
+  else waitcnt_vm<9>();
+  __builtin_amdgcn_s_barrier();
+  compiler_fence_gemm();
+  GemmFrags F0, F1;
+  {
+    const uint8_t* ta = smem + wm * 128 * G_FK;
+    const uint8_t* tb = smem + G_OPB + wn * 64 * G_FK;
+#pragma unroll
+    for (int i = 0; i < G_NI; ++i) F0.w[i] = read_frag(tb + i * 32 * G_FK, roff[0][0], roff[0][1]);
+#pragma unroll
+    for (int j = 0; j < G_NJ; ++j) F0.x[j] = read_frag(ta + j * 32 * G_FK, roff[0][0], roff[0][1]);
+  }
+
+  const float sa_t = g.sa[0], sb_t = g.sb[0];  // per-tensor scales
+  int S = 0;
+  for (int t = 0; t < my_tiles; ++t) {
+    for (int sl = 0; sl < nks; ++sl, ++S) {
+      // sub-step (S, 0): MFMAs of F0, reads of (S, 1) from this stage's slot
+      compute(F0, F1, S & 1, std::integral_constant<int, 1>{});
+      // sub-step (S, 1): stage S + 1 landed (this wavefront's fills, and after
+      // the barrier everyone's); this stage's slot is free for stage S + 2
+      compiler_fence_gemm();
+      if (sl == 0 && t > 0) waitcnt_vm<EPI_STORES>();  // the previous tile's stores are newer
+      else waitcnt_vm<0>();
+      __builtin_amdgcn_s_barrier();
+      compiler_fence_gemm();
+      if (S + 2 < n_total) fill_next();
+      compute(F1, F0, (S + 1) & 1, std::integral_constant<int, 0>{});
+    }
+
+    // ---- epilogue of tile t
+    int m0, n0;
+    coords(t, m0, n0);
+    const int rows = min(GT, g.M - m0);
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(g.out + (int64_t)m0 * g.ldo), (short)0, (int)(rows * g.ldo * 2), 0x00020000);
+    // lane-derived values are recomputed here, not held across the K loop
+    int lane_e = lane;
+    asm volatile("" : "+v"(lane_e));
+    const int mrow = lane_e & 31;
+    const int hh = lane_e >> 5;
+    const uint8_t* epi = smem + G_EPI_OFF + (t % 3) * G_EPI_REG;
+    uint8_t* stg = smem + G_STG_OFF + wave * 2048;
+    const int wswz = (mrow >> 1) & 3;
+    const int rb_row = lane_e >> 2, rb_c = lane_e & 3;  // read back 16 rows x 4 chunks per pass
+    uint32_t amax = 0;
+#pragma unroll
+    for (int j = 0; j < G_NJ; ++j) {
+      // acc[i][j]: lane l holds row m = wm 128 + 32 j + (l & 31), columns
+      // 32 i + 8 q + 4 (l >> 5) + r, r < 4, of the wavefront's 64
+      const int ml_w = wm * 128 + j * 32 + mrow;
+      const bool mok = ml_w < rows;
+      const float sa = g.sa_per_row ? *reinterpret_cast<const float*>(epi + 4 * ml_w) : sa_t;
+#pragma unroll
+      for (int i = 0; i < G_NI; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int nl = wn * 64 + i * 32 + 8 * q + 4 * hh;
+          const bool nok = n0 + nl < g.N;
+          float sb[4], bias[4];
+          if (g.sb_per_col) {
+            const float4 v = *reinterpret_cast<const float4*>(epi + 1024 + 4 * nl);
+            sb[0] = v.x; sb[1] = v.y; sb[2] = v.z; sb[3] = v.w;
+          } else {
+            sb[0] = sb[1] = sb[2] = sb[3] = sb_t;
+          }
+          if (g.bias) {
+            const uint2 bv = *reinterpret_cast<const uint2*>(epi + 2048 + 2 * nl);
+            bias[0] = __uint_as_float(bv.x << 16);
+            bias[1] = __uint_as_float(bv.x & 0xffff0000u);
+            bias[2] = __uint_as_float(bv.y << 16);
+            bias[3] = __uint_as_float(bv.y & 0xffff0000u);
+          } else {
+            bias[0] = bias[1] = bias[2] = bias[3] = 0.f;
+          }
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * q + r] * sa * sb[r] + bias[r];
+          typedef float f32x2v __attribute__((ext_vector_type(2)));
+          typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+          bf16x2v p0 = __builtin_convertvector(f32x2v{v[0], v[1]}, bf16x2v);
+          bf16x2v p1 = __builtin_convertvector(f32x2v{v[2], v[3]}, bf16x2v);
+          if (EPI == 1) {
+            const uint32_t b0 = __builtin_bit_cast(uint32_t, p0), b1 = __builtin_bit_cast(uint32_t, p1);
+            const float r0_ = __uint_as_float(b0 << 16), r1_ = __uint_as_float(b0 & 0xffff0000u);
+            const float r2_ = __uint_as_float(b1 << 16), r3_ = __uint_as_float(b1 & 0xffff0000u);
+            p0 = __builtin_convertvector(f32x2v{gelu_tanh(r0_), gelu_tanh(r1_)}, bf16x2v);
+            p1 = __builtin_convertvector(f32x2v{gelu_tanh(r2_), gelu_tanh(r3_)}, bf16x2v);
+          }
+          const uint32_t px = __builtin_bit_cast(uint32_t, p0), py = __builtin_bit_cast(uint32_t, p1);
+          if (AMAX && mok && nok) {
+            amax = max(amax, max((px & 0x7fffu) << 16, px & 0x7fff0000u));
+            amax = max(amax, max((py & 0x7fffu) << 16, py & 0x7fff0000u));
+          }
+          *reinterpret_cast<uint2*>(stg + mrow * 64 + 16 * (q ^ wswz) + 8 * hh) = make_uint2(px, py);
+        }
+        // the 32 x 32 block back as 16 rows x 64 bytes per store
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int rr = 16 * p + rb_row;
+          const i32x4_t d =
+              *reinterpret_cast<const i32x4_t*>(stg + rr * 64 + 16 * (rb_c ^ ((rr >> 1) & 3)));
+          const int ml = wm * 128 + j * 32 + rr;
+          const int n = n0 + wn * 64 + i * 32 + 8 * rb_c;
+          const int off = n < g.N ? (int)((ml * g.ldo + n) * 2) : (int)0x80000000;
+          __builtin_amdgcn_raw_buffer_store_b128(d, ro, off, 0, 0);
+        }
+      }
+    }
+    if (AMAX) {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, o));
+      if (lane == 0) raise_max_word(g.amax_out, amax);
+    }
+#pragma unroll
+    for (int i = 0; i < G_NI; ++i)
+#pragma unroll
+      for (int j = 0; j < G_NJ; ++j) acc[i][j] = f32x16_t{};
+  }
 }
 
 template <typename Launch>
@@ -630,9 +737,24 @@ extern "C" int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64
 }
 
 namespace srdit {
-int lt_fp8_gemm(const void* a, const void* b, const float* sa, const float* sb, const void* bias,
-                void* out, int64_t M, int64_t N, int64_t K, int64_t ldo, hipStream_t stream);
 namespace {
+// Compute units of the current device (cached per device): the GEMM runs one
+// persistent workgroup per CU.
+int cu_count_of_current_device() {
+  static std::mutex mu;
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cache[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_rows, const float* sb,
                     int64_t sb_cols, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
                     int64_t ldo, int epilogue, uint32_t* amax_out, void* stream, const char* who) {
@@ -640,8 +762,8 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
   SRDIT_REQUIRE(M > 0 && N > 0 && K > 0, "%s: M, N, K must be positive", who);
   SRDIT_REQUIRE(K % 128 == 0, "%s: K=%lld must be a multiple of 128", who, (long long)K);
   SRDIT_REQUIRE(N % 16 == 0, "%s: N=%lld must be a multiple of 16", who, (long long)N);
-  SRDIT_REQUIRE(ldo >= N && ldo % 4 == 0, "%s: ldo=%lld must be >= N and a multiple of 4", who,
-                (long long)ldo);
+  SRDIT_REQUIRE(ldo >= N && ldo % 8 == 0 && ldo < (int64_t(1) << 22),
+                "%s: ldo=%lld must be >= N, a multiple of 8 and below 2^22", who, (long long)ldo);
   SRDIT_REQUIRE(M * K < (int64_t(1) << 31) && N * K < (int64_t(1) << 31),
                 "%s: M*K and N*K must be below 2^31 (M=%lld N=%lld K=%lld)", who, (long long)M,
                 (long long)N, (long long)K);
@@ -649,18 +771,15 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
                 (long long)sa_rows);
   SRDIT_REQUIRE(sb_cols == 1 || sb_cols == N, "%s: sb_cols=%lld must be 1 or N", who,
                 (long long)sb_cols);
-  SRDIT_REQUIRE(aligned16(a) && aligned16(b) && aligned16(sb) && aligned16(out) &&
-                    (!bias || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0),
-                "%s: a, b, sb, out must be 16-byte aligned and bias 8-byte aligned", who);
-  const bool force_mfma = (epilogue & SRDIT_GEMM_MFMA) != 0;
+  // per-row / per-column scales and the bias reach LDS by 16-byte DMAs
+  SRDIT_REQUIRE(aligned16(a) && aligned16(b) && aligned16(out) && (!bias || aligned16(bias)) &&
+                    (sa_rows == 1 || aligned16(sa)) && (sb_cols == 1 || aligned16(sb)),
+                "%s: a, b, out, bias and per-row/per-column scales must be 16-byte aligned", who);
+  // SRDIT_GEMM_MFMA selected the hand-written kernel when plain GEMMs went to a
+  // library; every GEMM runs on it now, so the flag is accepted and ignored.
   epilogue &= ~SRDIT_GEMM_MFMA;
   SRDIT_REQUIRE(epilogue == 0 || epilogue == 1, "%s: epilogue %d is not 0 (none) or 1 (gelu)", who,
                 epilogue);
-  // Plain GEMMs with per-tensor scales go to hipBLASLt; the MFMA kernel below
-  // runs the fused epilogues, row-wise scales and what hipBLASLt declines.
-  if (!force_mfma && epilogue == 0 && !amax_out && sa_rows == 1 && sb_cols == 1 &&
-      lt_fp8_gemm(a, b, sa, sb, bias, out, M, N, K, ldo, static_cast<hipStream_t>(stream)) == 0)
-    return SRDIT_OK;
   GemmArgs g;
   g.a = static_cast<const uint8_t*>(a);
   g.b = static_cast<const uint8_t*>(b);
@@ -684,12 +803,15 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
     clear_u32_kernel<<<1, 1, 0, s>>>(amax_out);
     SRDIT_LAUNCH_CHECK("clear_u32_kernel");
   }
-  const unsigned grid = (unsigned)tiles;
-  if (epilogue == 0 && !amax_out) fp8_gemm_wide_kernel<0, false><<<grid, 512, 0, s>>>(g);
-  else if (epilogue == 0) fp8_gemm_wide_kernel<0, true><<<grid, 512, 0, s>>>(g);
-  else if (!amax_out) fp8_gemm_wide_kernel<1, false><<<grid, 512, 0, s>>>(g);
-  else fp8_gemm_wide_kernel<1, true><<<grid, 512, 0, s>>>(g);
-  SRDIT_LAUNCH_CHECK("fp8_gemm_wide_kernel");
+  // one workgroup per CU, a multiple of 8 (one share per XCD), no more than the tiles need
+  const int64_t cus = (cu_count_of_current_device() / 8) * 8;
+  const int64_t need = (tiles + 7) / 8 * 8;
+  const unsigned grid = (unsigned)(cus >= 8 ? (need < cus ? need : cus) : 8);
+  if (epilogue == 0 && !amax_out) fp8_gemm_kernel<0, false><<<grid, 512, 0, s>>>(g);
+  else if (epilogue == 0) fp8_gemm_kernel<0, true><<<grid, 512, 0, s>>>(g);
+  else if (!amax_out) fp8_gemm_kernel<1, false><<<grid, 512, 0, s>>>(g);
+  else fp8_gemm_kernel<1, true><<<grid, 512, 0, s>>>(g);
+  SRDIT_LAUNCH_CHECK("fp8_gemm_kernel");
   return SRDIT_OK;
 }
 }  // namespace
@@ -736,7 +858,6 @@ namespace srdit {
 namespace {
 std::mutex g_lut_mu;
 void* g_lut_dev[64] = {};
-int g_cus_dev[64] = {};
 
 int gelu_lut_of_current_device(void** out, const char* who) {
   int dev = -1;
@@ -753,21 +874,12 @@ int gelu_lut_of_current_device(void** out, const char* who) {
       return SRDIT_EHIP;
     }
     g_lut_dev[dev] = p;
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    g_cus_dev[dev] = n;
   }
   *out = g_lut_dev[dev];
   return SRDIT_OK;
 }
 
-int device_cu_count() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  std::lock_guard<std::mutex> lock(g_lut_mu);
-  return g_cus_dev[dev] > 0 ? g_cus_dev[dev] : 256;
-}
+int device_cu_count() { return cu_count_of_current_device(); }
 }  // namespace
 }  // namespace srdit
 

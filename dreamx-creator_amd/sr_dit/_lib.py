@@ -253,22 +253,21 @@ def fp8_gemm(a, b, sa, sb, bias, out):
     _check(rc, "srdit_fp8_gemm")
 
 
-#: epilogue flag of srdit_fp8_gemm_ex: run the hand-written MFMA kernel even for
-#: a plain per-tensor GEMM (which otherwise goes to hipBLASLt)
+#: epilogue flag of srdit_fp8_gemm_ex kept for old callers; it has no effect
+#: (every GEMM runs on the hand-written MFMA kernel)
 GEMM_MFMA = 0x100
 
 
-def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None, force_mfma=False):
-    """fp8_gemm with an epilogue (0 none, 1 GELU-tanh), an optional amax word and
-    an optional request for the MFMA kernel."""
+def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None):
+    """fp8_gemm with an epilogue (0 none, 1 GELU-tanh) and an optional amax word
+    (cleared by the call, then the bits of max |out|)."""
     M, K = a.shape
     N = b.shape[0]
     if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
         raise ValueError(f"fp8_gemm_ex: out must be bf16 [{M}, {N}] with unit column stride")
     rc = load().srdit_fp8_gemm_ex(_ptr(a), _ptr(b), _ptr(sa), int(sa.numel()), _ptr(sb),
                                   int(sb.numel()), _ptr(bias), _ptr(out), M, N, K, out.stride(0),
-                                  int(epilogue) | (GEMM_MFMA if force_mfma else 0),
-                                  _ptr(amax_out), _stream(a.device))
+                                  int(epilogue), _ptr(amax_out), _stream(a.device))
     _check(rc, "srdit_fp8_gemm_ex")
 
 

@@ -26,8 +26,7 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
              "-Wno-unused-command-line-argument"]
 # Per-source additions.  The window kernels keep their MFMA results and
 # accumulators in the VGPR form: a lazily rescaled O accumulator is otherwise
-# mirrored between AGPRs and VGPRs every step.  The GEMM needs the AGPRs for its
-# 256 accumulator registers per lane, so it keeps the default.
+# mirrored between AGPRs and VGPRs every step.  The GEMM keeps the default.
 FILE_FLAGS = {"window_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
               "window_group.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
               # the fused elementwise kernels round after every operation, as
@@ -83,9 +82,7 @@ def build(verbose: bool = False) -> str:
                      f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj])
     _run(cmds, verbose)
     tmp = OUT + ".tmp"
-    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
-    _run([[cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, f"-L{rocm}/lib", "-lhipblaslt",
-           f"-Wl,-rpath,{rocm}/lib", "-o", tmp]], verbose)
+    _run([[cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]], verbose)
     os.replace(tmp, OUT)
     return OUT
 

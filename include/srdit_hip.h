@@ -232,7 +232,10 @@ int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64_t ldx, int
  * out_dtype=bf16) in Fp8Linear.forward (fp8_linear.py:282-297); the bias is
  * applied to the fp32 value before the single bf16 rounding, as the reference's
  * epilogue does (fp8_linear.py:238-241).
- * Requires K % 128 == 0, N % 16 == 0, ldo % 4 == 0, M*K and N*K below 2^31.
+ * Runs on one hand-written MFMA kernel for every shape and scale mode (one
+ * persistent workgroup per CU).  Requires K % 128 == 0, N % 16 == 0,
+ * ldo % 8 == 0 and below 2^22, M*K and N*K below 2^31; a, b, out and bias
+ * 16-byte aligned, and sa / sb too when they hold one scale per row / column.
  */
 int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_rows,
                    const float* sb, int64_t sb_cols, const void* bias, void* out,
@@ -261,8 +264,9 @@ int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx
                                 int64_t ldh, void* xq, float* scale, uint32_t* amax_ws,
                                 void* stream);
 
-/* Flag for the epilogue argument of srdit_fp8_gemm_ex: run the hand-written
- * MFMA kernel even where the plain-GEMM library path would be taken. */
+/* Flag for the epilogue argument of srdit_fp8_gemm_ex, kept for callers that
+ * still pass it: it once selected the hand-written kernel over a library path.
+ * Every GEMM runs on that kernel now; the flag is accepted and has no effect. */
 #define SRDIT_GEMM_MFMA 0x100
 
 int srdit_fp8_gemm_ex(const void* a, const void* b, const float* sa, int64_t sa_rows,

@@ -156,13 +156,11 @@ TENSOR_CASES = [
 ]
 
 
-@pytest.mark.parametrize("backend", ["auto", "mfma"])
 @pytest.mark.parametrize("M,N,K,use_bias,ldo", TENSOR_CASES, ids=lambda v: str(v))
-def test_gemm_per_tensor_both_backends(M, N, K, use_bias, ldo, backend):
-    """Per-tensor scales: the plain-GEMM library path ("auto") and the MFMA
-    kernel, each against the dequantised product with the per-element bound;
-    padding columns of a strided output stay untouched."""
-    print(f"gemm per-tensor {backend} M={M} N={N} K={K} bias={use_bias} ldo={ldo}", flush=True)
+def test_gemm_per_tensor(M, N, K, use_bias, ldo):
+    """Per-tensor scales against the dequantised product with the per-element
+    bound; padding columns of a strided output stay untouched."""
+    print(f"gemm per-tensor M={M} N={N} K={K} bias={use_bias} ldo={ldo}", flush=True)
     a, _ = _quant_codes((M, K), seed=M + 2 * K)
     b, _ = _quant_codes((N, K), seed=N + 5 * K)
     sa, sb = np.float32([0.75]), np.float32([1.25 / 64])
@@ -173,8 +171,7 @@ def test_gemm_per_tensor_both_backends(M, N, K, use_bias, ldo, backend):
     out = buf[:, :N]
     _lib().fp8_gemm_ex(torch.from_numpy(a).view(F8).cuda(), torch.from_numpy(b).view(F8).cuda(),
                        torch.from_numpy(sa).cuda(), torch.from_numpy(sb).cuda(),
-                       bias.cuda() if bias is not None else None, out,
-                       force_mfma=(backend == "mfma"))
+                       bias.cuda() if bias is not None else None, out)
     torch.cuda.synchronize()
     if M * N <= 4_000_000:
         _gemm_check(out, a, b, sa, sb, bias.float().numpy() if bias is not None else None)
@@ -224,6 +221,62 @@ def test_gemm_full_size_against_fp32_matmul(M, N, K):
     tol = 2.0 ** -8 * ref.abs() + 2.0 ** -12 * absum + 2.0 ** -20 * absum.max()
     worst = ((out.float() - ref).abs() / tol).max().item()
     assert worst <= 1.0, worst
+
+
+MULTI_TILE_CASES = [
+    # M, N, K, row-wise scales, ldo (None: N): more tiles than CUs, so each
+    # persistent workgroup walks several tiles (one or two K stages per tile,
+    # ragged last rows and columns, a strided output)
+    (5000, 4096, 128, True, None),
+    (3000, 6144, 256, True, None),
+    (4100, 4624, 384, False, 4640),
+]
+
+
+def _dequant_check(out, aq, bq, sa, sb, bias, epilogue=0):
+    torch.backends.cuda.matmul.allow_tf32 = False
+    A, B = aq.float(), bq.float()
+    sa_ = sa.reshape(-1, 1) if sa.numel() > 1 else sa.reshape(())
+    sb_ = sb.reshape(1, -1) if sb.numel() > 1 else sb.reshape(())
+    ref = (A @ B.T) * sa_ * sb_ + bias.float()
+    absum = (A.abs() @ B.abs().T) * sa_.abs() * sb_.abs()
+    tol = 2.0 ** -8 * ref.abs() + 2.0 ** -12 * absum + 2.0 ** -20 * absum.max()
+    worst = ((out.float() - ref).abs() / tol).max().item()
+    assert worst <= 1.0, worst
+
+
+@pytest.mark.parametrize("M,N,K,rs,ldo", MULTI_TILE_CASES, ids=lambda v: str(v))
+def test_gemm_persistent_multi_tile(M, N, K, rs, ldo):
+    print(f"gemm multi-tile M={M} N={N} K={K} rowwise={rs} ldo={ldo}", flush=True)
+    g = torch.Generator("cpu").manual_seed(M + N + K)
+    a = (torch.randn(M, K, generator=g) * 0.6).to(F8).cuda()
+    b = (torch.randn(N, K, generator=g) * 0.6).to(F8).cuda()
+    if rs:
+        sa = (torch.rand(M, generator=g) + 0.5).cuda()
+        sb = (torch.rand(N, generator=g) / 64 + 1 / 128).cuda()
+    else:
+        sa, sb = torch.tensor([0.75]).cuda(), torch.tensor([1.25 / 64]).cuda()
+    bias = (torch.randn(N, generator=g) * 2).to(torch.bfloat16).cuda()
+    lo = ldo or N
+    buf = torch.full((M, lo), 7.0, dtype=torch.bfloat16, device="cuda")
+    out = buf[:, :N]
+    _lib().fp8_gemm(a, b, sa, sb, bias, out)
+    torch.cuda.synchronize()
+    _dequant_check(out, a, b, sa, sb, bias)
+    if lo > N:
+        assert torch.all(buf[:, N:] == 7.0)
+    # the GELU epilogue with the output's amax over the same tiles
+    out2 = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    amax = torch.full((1,), 12345, dtype=torch.int32, device="cuda")
+    _lib().fp8_gemm_ex(a, b, sa, sb, bias, out2, epilogue=1, amax_out=amax)
+    plain = out.contiguous()
+    gel = torch.nn.functional.gelu(plain.float(), approximate="tanh").to(torch.bfloat16)
+    torch.cuda.synchronize()
+    # the epilogue rounds to bf16, then GELU, then bf16; 1 + tanh(.) cancels for
+    # negative inputs, so bound by the input's magnitude
+    err = (out2.float() - gel.float()).abs()
+    assert (err <= 5e-3 * plain.float().abs() + 1e-30).all(), err.max().item()
+    assert amax.item() == out2.float().abs().max().view(torch.int32).item()
 
 
 def test_fp8_linear_rowwise_and_tensor():

@@ -31,7 +31,7 @@ def _existing(x, w, ws, b):
     amax = torch.zeros(1, dtype=torch.int32, device=DEV)
     _lib.fp8_quant_tensor(x, xq, scale, amax)
     out = torch.empty(M, w.shape[0], dtype=torch.bfloat16, device=DEV)
-    _lib.fp8_gemm_ex(xq, w, scale, ws, b, out, force_mfma=True)
+    _lib.fp8_gemm_ex(xq, w, scale, ws, b, out)
     return out
 
 
