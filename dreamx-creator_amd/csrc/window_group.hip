@@ -856,6 +856,9 @@ int group_entry(const char* fn, const void* q, const void* k, const void* v, voi
   SRDIT_REQUIRE(static_cast<int64_t>(H) * W < (1LL << 22), "%s: grid too large", fn);
   SRDIT_REQUIRE(kv_tokens * n_heads * head_dim * 2 < (1LL << 31),
                 "%s: K/V must span fewer than 2^31 bytes", fn);
+  // Q and O are read and written through structured buffers too
+  SRDIT_REQUIRE(q_tokens * n_heads * head_dim * 2 < (1LL << 31),
+                "%s: Q/O must span fewer than 2^31 bytes", fn);
   SRDIT_REQUIRE(static_cast<int64_t>(n_heads) * head_dim * 2 < (1LL << 14),
                 "%s: token stride n_heads*head_dim*2 must be below 16384 "
                 "bytes (structured-buffer stride)", fn);

@@ -40,10 +40,6 @@ SIGNATURES = {
                                               _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64,
                                               _c_int, _c_int, _c_f, _c_int, _c_int, _c_p,
                                               _c_p, _c_int, _c_p]),
-    "srdit_window_attn_shared_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
-                                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64,
-                                              _c_i64, _c_int, _c_int, _c_f, _c_int, _c_int, _c_p,
-                                              _c_p, _c_int, _c_int, _c_p]),
     "srdit_fp8_quant_rowwise": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p]),
     "srdit_fp8_quant_tensor": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
                                         _c_p]),
@@ -178,22 +174,6 @@ def window_attn_packed_fwd(q, k, v, o, params, tiles, *, n_w, hr_base, H, W, n_h
 
 
 QUANT_DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
-
-
-def window_attn_shared_fwd(q, k, v, o, params, sched, *, n_w, hr_base, H, W, n_heads, head_dim,
-                           kv_tokens, scale, ring=None, amax_out=None):
-    """The shared-fetch window kernel; ``sched`` holds the device tables
-    ``groups``, ``step_off`` and ``steps`` built by ``kv_share.build_share_schedule``."""
-    if q.dtype not in DTYPE_CODES:
-        raise ValueError(f"window attention needs bf16 or fp16, got {q.dtype}")
-    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(params), _ptr(sched["groups"]),
-            _ptr(sched["step_off"]), _ptr(sched["steps"]), int(n_w), int(sched["n_groups"]),
-            int(hr_base), int(H), int(W), int(q.shape[0]), int(kv_tokens), int(n_heads),
-            int(head_dim), float(scale))
-    _check(load().srdit_window_attn_shared_fwd(*args, *_ex_args(ring, amax_out),
-                                               int(sched["members"]), DTYPE_CODES[q.dtype],
-                                               _stream(q.device)),
-           "srdit_window_attn_shared_fwd")
 
 
 def _quant_args(x, xq):

@@ -17,7 +17,6 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from . import kv_share
 
 # Params row layouts (int32, one row per window); the kernel reads them with
 # raw pointer arithmetic.  All lengths are lengths, not end indices.
@@ -166,16 +165,6 @@ def mean_kv_tokens(plan) -> float:
 #: 1024 context tokens, 78 vs 82 us up to 280 vs 315 us (one process, identical
 #: outputs), so no minimum applies.
 GROUPED_MIN_KV = 0
-
-
-#: ``kernel="auto"`` leaves the shared-fetch kernel off: in interleaved A/B runs
-#: on one MI355X it is slower than the one-member grouped kernel on c2-c4
-#: (c3: 455 us with two members, 515 us with four, against 402 us), though it
-#: moves half the K/V bytes: the barrier couples 4-8 wavefronts per step and
-#: the step control costs more SALU/VALU per MFMA.  ``kernel="shared"``
-#: (four members) and ``"shared2"`` (two) select it.
-SHARED_AUTO = False
-SHARED_MEMBERS = 2
 
 
 def launch_order(plan) -> torch.Tensor:
@@ -460,26 +449,6 @@ def paired_fraction(groups: torch.Tensor) -> float:
     return 2 * paired / (2 * paired + (n - paired))
 
 
-def _share_tables(plan, H, W, head_dim, device, members):
-    """The shared-fetch schedule of ``plan`` on ``device`` (built and copied once),
-    or None when the plan is not made of 4x8-token KV units."""
-    key = ("share", H, W, head_dim, members)
-    host = plan.get(key)
-    if host is None:
-        host = plan[key] = (kv_share.build_share_schedule(plan, H, W, members)
-                            if kv_share.share_supported(plan, H, W, head_dim) else False)
-    if host is False:
-        return None
-    dkey = ("share_dev", H, W, head_dim, members, device)
-    dev = plan.get(dkey)
-    if dev is None:
-        dev = plan[dkey] = {"groups": host["groups"].to(device),
-                            "step_off": host["step_off"].to(device),
-                            "steps": host["steps"].to(device), "n_groups": host["n_groups"],
-                            "members": host["members"]}
-    return dev
-
-
 def _device_tables(plan, device):
     """(params, order) on ``device``, copied once per plan and device."""
     key = ("dev", device)
@@ -502,20 +471,22 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     stride-1 head dim, on one device, bf16 or fp16.  The launch is
     asynchronous on the current stream.
 
-    ``kernel``: ``"auto"`` runs plain plans without an anchor prefix on the
-    grouped kernel: with two members per workgroup sharing their K/V fetches
-    (``"grouped"``) when the pairs share nearly all their KV frames (the two
-    m-tiles of one window, or the query tiles of dense attention) and the
-    windows average at least ``GROUPED_MIN_KV`` KV tokens, else with one
-    member per workgroup (``"solo"``).
-    Anchored plans run solo too (the anchor frames walked after the HR
-    frames); plans beyond its limits (more than 16 HR frames per window, more
-    than 32 frame slots) go to the single-window kernel (``"single"``).
-    Measured on one MI355X: c2 and c3 (neighbouring-frame pairs sharing 2 of
-    3 frames) and the 48-query shipped windows run fastest solo; c4 (m-tile
-    pairs) and dense attention over the text context grouped.  Any of the three can be forced (a forced grouped launch
-    of an anchored plan raises, as does a forced solo launch of a plan beyond
-    its limits).
+    ``kernel``: one of ``"auto"``, ``"grouped"``, ``"solo"``, ``"packed"`` and
+    ``"single"``.  ``"auto"`` chooses as follows:
+    - plain plans (no anchor prefix, at most 16 KV frames per window) whose
+      64-query members pair up sharing at least 90% of their KV frames (the two
+      m-tiles of one window, the query tiles of dense attention over the text
+      context) run two members per workgroup (``"grouped"``);
+    - other plain plans run one member per workgroup: on packed tiles, two
+      neighbouring windows to a 64-row tile (``"packed"``), when that removes
+      at least ``PACKED_MIN_SAVING`` of the one-window tiles (the 48-query
+      windows of the shipped 4x4-block geometry), else one window per tile
+      (``"solo"``: c2 and c3);
+    - anchored plans run solo (the anchor frames walked after the HR frames)
+      when they have at most 16 HR frames and 32 frame slots per window;
+    - anything else runs on the single-window kernel (``"single"``).
+    Forcing ``"grouped"`` for an anchored plan, ``"solo"`` beyond its limits or
+    ``"packed"`` for a plan with nothing to pack raises ``ValueError``.
 
     ``ring`` = ``(ring_frames, ring_cached, head)``: the HR KV after the anchor
     prefix is an in-place cache (``sr_dit.kv_ring.KVRing``): ``ring_frames``
@@ -547,9 +518,9 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
     mode = 1 if anchor_mode == "frame" else 0
     if (plan["p_stride"] == P_FRAME) != (mode == 1):
         raise ValueError("run_blockgrid_hip: plan layout does not match anchor_mode.")
-    if kernel not in ("auto", "shared", "shared2", "grouped", "solo", "single", "packed"):
-        raise ValueError("run_blockgrid_hip: kernel must be auto, shared, shared2, grouped, solo, "
-                         f"single or packed, got {kernel!r}")
+    if kernel not in ("auto", "grouped", "solo", "single", "packed"):
+        raise ValueError("run_blockgrid_hip: kernel must be auto, grouped, solo, single or packed, "
+                         f"got {kernel!r}")
     if kernel == "packed":
         tiles = _packed_table(plan, q.device) if anchor_mode is None else None
         if tiles is None:
@@ -561,19 +532,6 @@ def run_blockgrid_hip(q, k_ext, v_ext, out, *, plan, f_cur, h, w, n, d,
             n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0], scale=d ** -0.5, ring=ring,
             amax_out=amax_out)
         return out
-    if kernel in ("auto", "shared", "shared2"):
-        members = 2 if kernel == "shared2" else (SHARED_MEMBERS if kernel == "auto" else 4)
-        share = (_share_tables(plan, h, w, d, q.device, members)
-                 if anchor_mode is None and plan["p_stride"] == P_PLAIN else None)
-        if share is not None and (kernel != "auto" or SHARED_AUTO):
-            _lib.window_attn_shared_fwd(
-                q, k_ext, v_ext, out, params, share, n_w=plan["n_w"], hr_base=hr_base, H=h, W=w,
-                n_heads=n, head_dim=d, kv_tokens=k_ext.shape[0], scale=d ** -0.5, ring=ring,
-                amax_out=amax_out)
-            return out
-        if kernel != "auto":
-            raise ValueError("run_blockgrid_hip: the shared-fetch kernel needs plain rows without "
-                             "an anchor, head_dim 128 and KV cuboids made of 4x8-token units.")
     if kernel == "grouped" and not groups_supported(plan):
         raise ValueError("run_blockgrid_hip: the grouped kernel needs plain rows without an anchor.")
     if kernel == "solo" and not solo_supported(plan):

@@ -158,45 +158,6 @@ int srdit_window_attn_packed_fwd(const void* q, const void* k, const void* v, vo
                                  void* stream);
 
 /*
- * Block-grid window attention, forward, with K/V fetches shared between
- * neighbouring windows: up to `members` (2 or 4) 64-query members per
- * workgroup of 2*members wavefronts walk a host-built step schedule, and each
- * 32-key unit (4 token
- * rows x 8 token columns of one KV frame) that several members read in a step
- * is moved from L2 into LDS once.
- *
- * Replaces the same launch as srdit_window_attn_fwd mode 0
- * (run_blockgrid_triton -> _blockgrid_fused_kernel, blockgrid_triton.py:392-422,
- * :184-278) for plain tables without an anchor prefix whose KV cuboids are
- * unions of 4x8-token units (row extents starting on multiples of 4, column
- * extents on multiples of 8, ending on such multiples or at the grid edge):
- * the 8x8-block geometries.
- *
- * params      int32 [n_w, 19] device table (the planner's plain rows)
- * groups      int32 [n_groups, 8]: (row, m-tile) for four members, row -1 none
- * step_off    int32 [n_groups + 1]: first step of each workgroup in `steps`
- * steps       int32 [total steps, 16] step records: words 0-7 up to four fill
- *             units (frame << 24 | token offset of the unit in its frame,
- *             k_slot | v_slot << 8), words 8-11 per member k_slot | v_slot << 5
- *             | valid rows << 10 | valid columns << 13 (0: idle; a member's
- *             active steps come first), word 12 the number of fill units.
- *             Slots index one LDS pool of 5*members 8 KB tiles shared by K
- *             and V (indices are clamped into it); a fill issued at step s
- *             must not target a slot read at step s or later.
- * The schedule decides which keys each member attends: a malformed one gives
- * wrong numbers; every token index is clamped into the K/V tensors.
- * ring_frames, ring_cached, ring_head, amax_out as srdit_window_attn_fwd_ex.
- * head_dim 128 only.  Other arguments as srdit_window_attn_fwd.
- */
-int srdit_window_attn_shared_fwd(const void* q, const void* k, const void* v, void* o,
-                                 const int32_t* params, const int32_t* groups,
-                                 const int32_t* step_off, const int32_t* steps, int n_w,
-                                 int n_groups, int hr_base, int H, int W, int64_t q_tokens,
-                                 int64_t kv_tokens, int n_heads, int head_dim, float scale,
-                                 int ring_frames, int ring_cached, const int32_t* ring_head,
-                                 uint32_t* amax_out, int members, int dtype, void* stream);
-
-/*
  * Row-wise fp8 e4m3 quantiser: for each row of x [M, K] (row stride ldx),
  *   scale[m] = max(amax(|x[m,:]|) * fl32(1/448), 1e-12)   (fp32; what torch computes
  *              for amax / 448.0 on a GPU tensor)

@@ -68,3 +68,31 @@ def test_copy_rejects_misaligned_size():
     lib = _lib.load()
     fake = ctypes.c_void_p(4096)
     assert lib.srdit_copy_bytes(fake, fake, 15, None) == 1
+
+
+def test_grouped_window_rejects_a_q_span_past_2_31_without_gpu():
+    # 400,000 query tokens x 24 heads x 128 x 2 bytes > 2^31 while the K/V span
+    # (1,000 tokens) passes: refused before any HIP call
+    lib = _lib.load()
+    fake = ctypes.c_void_p(4096)
+    rc = lib.srdit_window_attn_grouped_fwd(fake, fake, fake, fake, fake, fake, 1, 1, 0, 1, 1,
+                                           400000, 1000, 24, 128, 0.088, 0, None)
+    assert rc == 1 and "Q/O" in _lib.last_error()
+
+
+def test_gemm_rejects_bad_layouts_without_gpu():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(4096)
+    # ldo must be a multiple of 8 (the output leaves as 16-byte row pieces)
+    rc = lib.srdit_fp8_gemm(fake, fake, fake, 1, fake, 1, None, fake, 64, 32, 256, 36, None)
+    assert rc == 1 and "ldo" in _lib.last_error()
+    # the bias reaches LDS by 16-byte DMAs
+    rc = lib.srdit_fp8_gemm(fake, fake, fake, 1, fake, 1, ctypes.c_void_p(4104), fake, 64, 32,
+                            256, 32, None)
+    assert rc == 1 and "aligned" in _lib.last_error()
+    # per-tensor scales may sit anywhere; per-row ones must be 16-byte aligned
+    rc = lib.srdit_fp8_gemm(fake, fake, ctypes.c_void_p(4100), 64, fake, 1, None, fake, 64, 32,
+                            256, 32, None)
+    assert rc == 1 and "aligned" in _lib.last_error()
+    rc = lib.srdit_fp8_gemm(fake, fake, fake, 1, fake, 1, None, fake, 64, 32, 200, 32, None)
+    assert rc == 1 and "K=200" in _lib.last_error()
