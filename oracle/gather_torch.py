@@ -6,14 +6,22 @@ Follows video_refiner/wan/modules/sr_dit/attention.py:
   * _win_attend              :650-657  F.scaled_dot_product_attention
   * _blockgrid_gather_attend :727-802  index_copy_ scatter, anchor columns
 Used as the CPU baseline of bench.py (timed on the host cores) and, in fp32 on
-the GPU, as the reference for full-size parity tests.  It is the checker, not
-the product: nothing under dreamx-creator_amd/ imports it.
+the GPU, as the reference for full-size parity tests.  There the tests pass
+``math_backend=True``, which pins SDPA to its math backend (an explicit
+softmax(q k^T * scale) v in the input dtype), so no fused or memory-efficient
+kernel of the library stands between the reference and the formula; a GPU test
+checks sampled windows of that reference against the float64 oracle
+(oracle/blockgrid.py).  It is the checker, not the product: nothing under
+dreamx-creator_amd/ imports it.
 """
 from __future__ import annotations
 
 import numpy as np
+import contextlib
+
 import torch
 import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import blockgrid as bg
 
@@ -37,8 +45,14 @@ class GatherPlan:
         self.n_q = g.f_cur * g.h * g.w
 
 
-def gather_attend(plan: GatherPlan, q, k_ext, v_ext, win_chunk=None):
-    """q [s, n, d], k_ext/v_ext [s_kv, n, d] -> [s, n, d] (same dtype as q)."""
+def gather_attend(plan: GatherPlan, q, k_ext, v_ext, win_chunk=None, math_backend=False):
+    """q [s, n, d], k_ext/v_ext [s_kv, n, d] -> [s, n, d] (same dtype as q).
+    ``math_backend``: run SDPA on its math backend only."""
+    with sdpa_kernel([SDPBackend.MATH]) if math_backend else contextlib.nullcontext():
+        return _gather_attend(plan, q, k_ext, v_ext, win_chunk)
+
+
+def _gather_attend(plan: GatherPlan, q, k_ext, v_ext, win_chunk):
     n, d = q.shape[1], q.shape[2]
     out = q.new_empty(plan.n_q, n, d)
     for g in plan.groups:

@@ -136,15 +136,18 @@ def test_block_stack_matches_fp32_restatement(scaling):
     assert err.max().item() <= 5e-2 * max(1.0, r.abs().max().item())
 
 
-def test_one_block_at_full_width_vs_gather_restatement():
+@pytest.mark.parametrize("scaling", ["tensor", "rowwise"])
+def test_one_block_at_full_width_vs_gather_restatement(scaling):
     """One block of the shipped width (3072, 24 heads of 128, FFN 14336, fp8
-    per-tensor) on the 6x45x80 token grid with 512 text tokens, against the
-    float32 restatement whose window attention is the gather backend
-    (oracle/gather_torch.py, attention.py:660-802) over the oracle's windows."""
+    per-tensor, or row-wise as the reference's Fp8Linear defaults to,
+    fp8_linear.py:93-103) on the 6x45x80 token grid with 512 text tokens,
+    against the float32 restatement whose window attention is the gather
+    backend (oracle/gather_torch.py, attention.py:660-802) over the oracle's
+    windows."""
     from oracle import gather_torch as ogt
     cfg = mdl.SRDiTConfig()
-    print("[case] one block at 3072 wide, 6x45x80 tokens, 512 text tokens", flush=True)
-    model = mdl.build_refiner(cfg, device=DEV, scaling="tensor", seed=5, num_layers=1)
+    print(f"[case] one block at 3072 wide, 6x45x80 tokens, 512 text tokens, {scaling}", flush=True)
+    model = mdl.build_refiner(cfg, device=DEV, scaling=scaling, seed=5, num_layers=1)
     f, h, w = 6, 45, 80
     geom = model.geometry(f, h, w, cfg.text_len, DEV)
     g = torch.Generator("cpu").manual_seed(2)
@@ -155,7 +158,8 @@ def test_one_block_at_full_width_vs_gather_restatement():
     plan = ogt.GatherPlan(geo, None, device=DEV)
 
     def attn(q, k, v):
-        return ogt.gather_attend(plan, q.float(), k.float(), v.float(), win_chunk=64).to(q.dtype)
+        return ogt.gather_attend(plan, q.float(), k.float(), v.float(), win_chunk=64,
+                                 math_backend=True).to(q.dtype)
 
     with torch.no_grad():
         out = model.blocks_forward(x, e0, ctx, geom)
@@ -189,6 +193,50 @@ def test_rope_fp32_matches_complex128():
     # boundary; such elements differ by one bf16 step
     assert (diff > 0).float().mean().item() < 1e-3
     assert diff.max().item() <= 2 ** -7 * ref.float().abs().max().item()
+
+
+def test_whole_30_layer_forward_graph_equals_eager():
+    """The whole refiner forward at the shipped size (models.py:1877-2002): time
+    and text embeddings, the patch embedding of a 48x6x90x160 latent, 30 blocks
+    (fp8 per-tensor), head and unpatchify.  Finite and deterministic; captured
+    once in a HIP graph, every replay (with eager work and synchronisations
+    between replays) equals the eager forward bit for bit, also after new
+    inputs are copied into the captured buffers."""
+    cfg = mdl.SRDiTConfig()
+    print("[case] whole 30-layer forward, graph vs eager", flush=True)
+    model = mdl.build_refiner(cfg, device=DEV, scaling="tensor", seed=0)
+    assert len(model.blocks) == 30
+    f, h, w = 6, 45, 80
+    geom = model.geometry(f, h, w, cfg.text_len, DEV)
+    g = torch.Generator("cpu").manual_seed(3)
+    latent = torch.randn(cfg.in_dim, f, 2 * h, 2 * w, generator=g).to(DEV)
+    ctx = torch.randn(cfg.text_len, cfg.text_dim, generator=g).to(torch.bfloat16).to(DEV)
+    t = torch.tensor([625.0], device=DEV)
+    with torch.no_grad():
+        want = model.forward(latent, t, ctx, geom)
+        again = model.forward(latent, t, ctx, geom)
+        torch.cuda.synchronize()
+        assert want.shape == (cfg.out_dim, f, 2 * h, 2 * w)
+        assert torch.isfinite(want).all() and want.float().std().item() > 0
+        assert torch.equal(want, again)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y = model.forward(latent, t, ctx, geom)
+        for i in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, want), f"replay {i}"
+            junk = torch.randn(1024, 1024, device=DEV) @ torch.randn(1024, 1024, device=DEV)
+            torch.cuda.synchronize()
+            del junk
+        # new inputs through the captured buffers
+        latent.copy_(torch.randn(latent.shape, generator=g).to(DEV))
+        t.fill_(250.0)
+        want2 = model.forward(latent, t, ctx, geom)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(want2).all() and not torch.equal(want2, want)
+        assert torch.equal(y, want2)
 
 
 def test_full_size_step_in_a_graph():

@@ -118,7 +118,38 @@ def test_anchor_plans_both_kernels_vs_float64_oracle(name, spec, mode, kernel):
 
 def _gather_ref(spec, mode, q, k_ext, v_ext):
     plan = ogt.GatherPlan(_geom_of(spec), mode, device=q.device)
-    return ogt.gather_attend(plan, q.float(), k_ext.float(), v_ext.float(), win_chunk=48)
+    return ogt.gather_attend(plan, q.float(), k_ext.float(), v_ext.float(), win_chunk=48,
+                             math_backend=True)
+
+
+def test_gpu_gather_reference_matches_float64_on_c3_windows():
+    """The full-size reference itself: the fp32 gather restatement on the GPU
+    (SDPA on its math backend) against the float64 oracle on a sample of c3
+    windows (corner, ragged last block row, interior, both edge columns, every
+    frame run), all 24 heads, peaky inputs."""
+    spec = wl.window_spec("c3")
+    geo = _geom_of(spec)
+    q, k, v, _, _ = wl.make_window_inputs("c3", torch.bfloat16, DEV, seed=11, temperature=8.0)
+    q, k, v = q[0].contiguous(), k[0].contiguous(), v[0].contiguous()
+    ref = _gather_ref(spec, None, q, k, v).double().cpu().numpy()
+    qn, kn, vn = (t.double().cpu().numpy() for t in (q, k, v))
+    wins = obg.windows(geo)
+    pick = sorted({0, 9, 50, 59, 60 * 2 + 33, 60 * 3 + 10, 60 * 5 + 59, len(wins) - 1})
+    worst = 0.0
+    for i in pick:
+        q_idx, kv_idx = wins[i]
+        qs = qn[q_idx].transpose(1, 0, 2)
+        ks = kn[kv_idx].transpose(1, 0, 2)
+        vs = vn[kv_idx].transpose(1, 0, 2)
+        sc = qs @ ks.transpose(0, 2, 1) * 128 ** -0.5
+        p = np.exp(sc - sc.max(-1, keepdims=True))
+        o = (p @ vs / p.sum(-1, keepdims=True)).transpose(1, 0, 2)
+        err = np.abs(ref[q_idx] - o).max() / max(1e-30, np.abs(o).max())
+        worst = max(worst, err)
+    print(f"[metrics] gather reference vs float64 on {len(pick)} c3 windows: "
+          f"max rel err {worst:.3e}", flush=True)
+    # fp32 accumulation over at most 1728 keys
+    assert worst < 1e-5, worst
 
 
 @pytest.mark.parametrize("cfg", ["c1", "c2", "c3", "c4"])

@@ -102,7 +102,7 @@ def test_packed_shipped_geometry_vs_fp32_gather(temp):
     print(f"[case] packed shipped temp={temp}", flush=True)
     out = _launch(spec, q, k, v, "packed")
     ref = ogt.gather_attend(ogt.GatherPlan(_geom_of(spec), None, device=q.device), q.float(),
-                            k.float(), v.float(), win_chunk=48)
+                            k.float(), v.float(), win_chunk=48, math_backend=True)
     check_attention(out, ref, label=f"packed_shipped_t{temp}")
 
 
