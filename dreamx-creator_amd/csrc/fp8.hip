@@ -199,6 +199,9 @@ struct GemmArgs {
   int sa_per_row, sb_per_col;
   int tiles_m, tiles_n;
   uint32_t* amax_out;  // AMAX epilogue only
+  // Split output (0: none): columns [j split_n, (j + 1) split_n) are stored at
+  // out + j split_stride as a block of rows of stride ldo.
+  int64_t split_n, split_stride;
 };
 
 __device__ __forceinline__ void compiler_fence_gemm() { asm volatile("" ::: "memory"); }
@@ -283,9 +286,23 @@ __device__ __forceinline__ uint32_t abs_bits_max_bf16x8(uint4 h, uint32_t m) {
   return m;
 }
 
+// Inputs whose largest positive value is at least this (0.375) have
+// max |h| = |h(that value)|: h is non-decreasing over x >= 0 and |h| <= 0.1700
+// below 0, while h(0.375) = 0.2373.
+constexpr uint32_t GELU_AMAX_SHORTCUT = 0x3ec00000u;
+
 __global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_amax_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx, uint16_t* __restrict__ h,
-    int64_t ldh, const uint16_t* __restrict__ lut, uint32_t* __restrict__ amax_ws) {
+    int64_t ldh, const uint16_t* __restrict__ lut, uint32_t* __restrict__ amax_ws,
+    const uint32_t* __restrict__ xmax_pos) {
+  if (xmax_pos) {  // the producer's largest positive value decides the amax on its own
+    const uint32_t key = *xmax_pos;
+    if (key >= GELU_AMAX_SHORTCUT) {
+      if (blockIdx.x == 0 && threadIdx.x == 0)
+        *amax_ws = static_cast<uint32_t>(lut[key >> 16] & 0x7fffu) << 16;
+      return;
+    }
+  }
   __shared__ __attribute__((aligned(16))) uint16_t tab[LUT_N];
   __shared__ uint32_t part[LUT_WAVES];
   load_lut_to_lds(tab, lut);
@@ -402,6 +419,14 @@ __global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_quant_kernel(
 // (2.33-2.36), 21600 x 3072 x 14336 in 760-790 us (2.41-2.50); without its
 // fills the same loop runs 2.85-3.3 PFLOP/s, where core-clock counters show the
 // MFMA pipe ~99% busy at the ~1.57 GHz the chip sustains under that load.
+// Order key of the largest positive value: the float bits of a non-negative
+// x (so +inf and larger values win), 0 for negative x, and 0x7fffffff for any
+// NaN, so a NaN anywhere makes the reduced key a NaN.
+__device__ __forceinline__ uint32_t pos_key(uint32_t bits) {
+  if ((bits & 0x7fffffffu) > 0x7f800000u) return 0x7fffffffu;
+  return (bits & 0x80000000u) ? 0u : bits;
+}
+
 constexpr int G_FK = 128;                      // K bytes per fill stage
 constexpr int G_OPB = GT * G_FK;               // one operand tile of a stage: 32 KB
 constexpr int G_SLOT = 2 * G_OPB;              // 64 KB
@@ -416,7 +441,10 @@ struct GemmFrags {
   i32x8_t w[G_NI], x[G_NJ];
 };
 
-template <int EPI, bool AMAX>
+// AMAX 0: none; 1: max |out| (float bits) into *g.amax_out; 2: the largest
+// positive output instead (0 if none, and the bits of a NaN when there is one),
+// which bounds the GELU of the output (srdit_fp8_quant_tensor_gelu_ex).
+template <int EPI, int AMAX>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fp8_gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G_LDS];
@@ -585,8 +613,18 @@ void fp8_gemm_kernel(const GemmArgs g) {
     int m0, n0;
     coords(t, m0, n0);
     const int rows = min(GT, g.M - m0);
+    // the tile's output base: row m0, and with a split output, shifted so that
+    // global column n of block j lands at out + j split_stride + (n - j split_n)
+    int64_t obase = (int64_t)m0 * g.ldo;
+    if (g.split_n) {
+      const int64_t blk = n0 / g.split_n;
+      obase += blk * (g.split_stride - g.split_n);
+    }
+    // every store offset of the tile, (row * ldo + column) * 2 for rows < rows
+    // and columns < N, stays below this bound
     const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(g.out + (int64_t)m0 * g.ldo), (short)0, (int)(rows * g.ldo * 2), 0x00020000);
+        (void*)(g.out + obase), (short)0, (int)(((int64_t)(rows - 1) * g.ldo + g.N) * 2),
+        0x00020000);
     // lane-derived values are recomputed here, not held across the K loop
     int lane_e = lane;
     asm volatile("" : "+v"(lane_e));
@@ -641,9 +679,12 @@ void fp8_gemm_kernel(const GemmArgs g) {
             p1 = __builtin_convertvector(f32x2v{gelu_tanh(r2_), gelu_tanh(r3_)}, bf16x2v);
           }
           const uint32_t px = __builtin_bit_cast(uint32_t, p0), py = __builtin_bit_cast(uint32_t, p1);
-          if (AMAX && mok && nok) {
+          if (AMAX == 1 && mok && nok) {
             amax = max(amax, max((px & 0x7fffu) << 16, px & 0x7fff0000u));
             amax = max(amax, max((py & 0x7fffu) << 16, py & 0x7fff0000u));
+          } else if (AMAX == 2 && mok && nok) {
+            amax = max(amax, max(pos_key(px << 16), pos_key(px & 0xffff0000u)));
+            amax = max(amax, max(pos_key(py << 16), pos_key(py & 0xffff0000u)));
           }
           *reinterpret_cast<uint2*>(stg + mrow * 64 + 16 * (q ^ wswz) + 8 * hh) = make_uint2(px, py);
         }
@@ -655,12 +696,12 @@ void fp8_gemm_kernel(const GemmArgs g) {
               *reinterpret_cast<const i32x4_t*>(stg + rr * 64 + 16 * (rb_c ^ ((rr >> 1) & 3)));
           const int ml = wm * 128 + j * 32 + rr;
           const int n = n0 + wn * 64 + i * 32 + 8 * rb_c;
-          const int off = n < g.N ? (int)((ml * g.ldo + n) * 2) : (int)0x80000000;
+          const int off = (n < g.N && ml < rows) ? (int)((ml * g.ldo + n) * 2) : (int)0x80000000;
           __builtin_amdgcn_raw_buffer_store_b128(d, ro, off, 0, 0);
         }
       }
     }
-    if (AMAX) {
+    if (AMAX != 0) {
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, o));
       if (lane == 0) raise_max_word(g.amax_out, amax);
@@ -757,13 +798,20 @@ int cu_count_of_current_device() {
 
 int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_rows, const float* sb,
                     int64_t sb_cols, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
-                    int64_t ldo, int epilogue, uint32_t* amax_out, void* stream, const char* who) {
+                    int64_t ldo, int epilogue, uint32_t* amax_out, void* stream, const char* who,
+                    int64_t split_n = 0, int64_t split_stride = 0) {
   SRDIT_REQUIRE(a && b && sa && sb && out, "%s: null pointer", who);
   SRDIT_REQUIRE(M > 0 && N > 0 && K > 0, "%s: M, N, K must be positive", who);
   SRDIT_REQUIRE(K % 128 == 0, "%s: K=%lld must be a multiple of 128", who, (long long)K);
   SRDIT_REQUIRE(N % 16 == 0, "%s: N=%lld must be a multiple of 16", who, (long long)N);
-  SRDIT_REQUIRE(ldo >= N && ldo % 8 == 0 && ldo < (int64_t(1) << 22),
-                "%s: ldo=%lld must be >= N, a multiple of 8 and below 2^22", who, (long long)ldo);
+  const int64_t width = split_n ? split_n : N;  // columns of one output block
+  SRDIT_REQUIRE(ldo >= width && ldo % 8 == 0 && (255 * ldo + N) * 2 + 16 < (int64_t(1) << 31),
+                "%s: ldo=%lld must be >= the output width, a multiple of 8, and keep 256 rows "
+                "below 2^31 bytes", who, (long long)ldo);
+  SRDIT_REQUIRE(split_n == 0 || (split_n % 256 == 0 && N % split_n == 0 && split_stride % 8 == 0 &&
+                                 split_stride >= M * ldo),
+                "%s: split_n=%lld must be a multiple of 256 dividing N, and split_stride=%lld a "
+                "multiple of 8 of at least M*ldo", who, (long long)split_n, (long long)split_stride);
   SRDIT_REQUIRE(M * K < (int64_t(1) << 31) && N * K < (int64_t(1) << 31),
                 "%s: M*K and N*K must be below 2^31 (M=%lld N=%lld K=%lld)", who, (long long)M,
                 (long long)N, (long long)K);
@@ -778,8 +826,12 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
   // SRDIT_GEMM_MFMA selected the hand-written kernel when plain GEMMs went to a
   // library; every GEMM runs on it now, so the flag is accepted and ignored.
   epilogue &= ~SRDIT_GEMM_MFMA;
+  const bool amax_pos = (epilogue & SRDIT_GEMM_AMAX_POS) != 0;
+  epilogue &= ~SRDIT_GEMM_AMAX_POS;
   SRDIT_REQUIRE(epilogue == 0 || epilogue == 1, "%s: epilogue %d is not 0 (none) or 1 (gelu)", who,
                 epilogue);
+  SRDIT_REQUIRE(!amax_pos || (amax_out && epilogue == 0),
+                "%s: SRDIT_GEMM_AMAX_POS needs amax_out and no GELU epilogue", who);
   GemmArgs g;
   g.a = static_cast<const uint8_t*>(a);
   g.b = static_cast<const uint8_t*>(b);
@@ -796,6 +848,8 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
   g.tiles_m = (int)((M + GT - 1) / GT);
   g.tiles_n = (int)((N + GT - 1) / GT);
   g.amax_out = amax_out;
+  g.split_n = split_n;
+  g.split_stride = split_stride;
   const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
   SRDIT_REQUIRE(tiles < (int64_t(1) << 31), "%s: too many tiles", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -807,10 +861,11 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
   const int64_t cus = (cu_count_of_current_device() / 8) * 8;
   const int64_t need = (tiles + 7) / 8 * 8;
   const unsigned grid = (unsigned)(cus >= 8 ? (need < cus ? need : cus) : 8);
-  if (epilogue == 0 && !amax_out) fp8_gemm_kernel<0, false><<<grid, 512, 0, s>>>(g);
-  else if (epilogue == 0) fp8_gemm_kernel<0, true><<<grid, 512, 0, s>>>(g);
-  else if (!amax_out) fp8_gemm_kernel<1, false><<<grid, 512, 0, s>>>(g);
-  else fp8_gemm_kernel<1, true><<<grid, 512, 0, s>>>(g);
+  if (epilogue == 0 && !amax_out) fp8_gemm_kernel<0, 0><<<grid, 512, 0, s>>>(g);
+  else if (epilogue == 0 && amax_pos) fp8_gemm_kernel<0, 2><<<grid, 512, 0, s>>>(g);
+  else if (epilogue == 0) fp8_gemm_kernel<0, 1><<<grid, 512, 0, s>>>(g);
+  else if (!amax_out) fp8_gemm_kernel<1, 0><<<grid, 512, 0, s>>>(g);
+  else fp8_gemm_kernel<1, 1><<<grid, 512, 0, s>>>(g);
   SRDIT_LAUNCH_CHECK("fp8_gemm_kernel");
   return SRDIT_OK;
 }
@@ -830,6 +885,16 @@ extern "C" int srdit_fp8_gemm_ex(const void* a, const void* b, const float* sa, 
                                  uint32_t* amax_out, void* stream) {
   return fp8_gemm_launch(a, b, sa, sa_rows, sb, sb_cols, bias, out, M, N, K, ldo, epilogue,
                          amax_out, stream, "srdit_fp8_gemm_ex");
+}
+
+extern "C" int srdit_fp8_gemm_split(const void* a, const void* b, const float* sa, int64_t sa_rows,
+                                    const float* sb, int64_t sb_cols, const void* bias, void* out,
+                                    int64_t M, int64_t N, int64_t K, int64_t ldo, int64_t split_n,
+                                    int64_t split_stride, void* stream) {
+  SRDIT_REQUIRE(split_n > 0, "srdit_fp8_gemm_split: split_n=%lld must be positive",
+                (long long)split_n);
+  return fp8_gemm_launch(a, b, sa, sa_rows, sb, sb_cols, bias, out, M, N, K, ldo, 0, nullptr,
+                         stream, "srdit_fp8_gemm_split", split_n, split_stride);
 }
 
 extern "C" int srdit_fp8_quant_apply(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype,
@@ -883,9 +948,11 @@ int device_cu_count() { return cu_count_of_current_device(); }
 }  // namespace
 }  // namespace srdit
 
-extern "C" int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx,
-                                           void* h, int64_t ldh, void* xq, float* scale,
-                                           uint32_t* amax_ws, void* stream) {
+namespace srdit {
+namespace {
+int quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx, void* h, int64_t ldh,
+                      void* xq, float* scale, uint32_t* amax_ws, const uint32_t* xmax_pos,
+                      void* stream) {
   if (int rc = check_quant_args("srdit_fp8_quant_tensor_gelu", x, M, K, ldx, xq, scale)) return rc;
   SRDIT_REQUIRE(amax_ws, "srdit_fp8_quant_tensor_gelu: null amax workspace");
   SRDIT_REQUIRE(!h || (aligned16(h) && ldh >= K && ldh % 8 == 0 && h != x),
@@ -901,13 +968,28 @@ extern "C" int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, 
   SRDIT_LAUNCH_CHECK("gelu_lut_build_kernel");
   gelu_lut_amax_kernel<<<blocks, 64 * LUT_WAVES, 0, s>>>(
       static_cast<const uint16_t*>(x), M, K, ldx, static_cast<uint16_t*>(h), ldh,
-      static_cast<const uint16_t*>(lut), amax_ws);
+      static_cast<const uint16_t*>(lut), amax_ws, h ? nullptr : xmax_pos);
   SRDIT_LAUNCH_CHECK("gelu_lut_amax_kernel");
   gelu_lut_quant_kernel<<<blocks, 64 * LUT_WAVES, 0, s>>>(
       static_cast<const uint16_t*>(x), M, K, ldx, static_cast<const uint16_t*>(lut),
       static_cast<uint8_t*>(xq), scale, amax_ws);
   SRDIT_LAUNCH_CHECK("gelu_lut_quant_kernel");
   return SRDIT_OK;
+}
+}  // namespace
+}  // namespace srdit
+
+extern "C" int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx,
+                                           void* h, int64_t ldh, void* xq, float* scale,
+                                           uint32_t* amax_ws, void* stream) {
+  return quant_tensor_gelu(x, M, K, ldx, h, ldh, xq, scale, amax_ws, nullptr, stream);
+}
+
+extern "C" int srdit_fp8_quant_tensor_gelu_ex(const void* x, int64_t M, int64_t K, int64_t ldx,
+                                              void* h, int64_t ldh, void* xq, float* scale,
+                                              uint32_t* amax_ws, const uint32_t* xmax_pos,
+                                              void* stream) {
+  return quant_tensor_gelu(x, M, K, ldx, h, ldh, xq, scale, amax_ws, xmax_pos, stream);
 }
 
 // ---------------------------------------------------------------------------

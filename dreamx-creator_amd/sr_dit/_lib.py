@@ -47,10 +47,14 @@ SIGNATURES = {
                                 _c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
     "srdit_fp8_gemm_ex": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p,
                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p]),
+    "srdit_fp8_gemm_split": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p,
+                                      _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
     "srdit_fp8_quant_apply": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
                                        _c_p]),
     "srdit_fp8_quant_tensor_gelu": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
                                              _c_p, _c_p, _c_p]),
+    "srdit_fp8_quant_tensor_gelu_ex": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
+                                                _c_p, _c_p, _c_p, _c_p, _c_p]),
     "srdit_ln_modulate": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_f,
                                    _c_p, _c_i64, _c_p, _c_p]),
     "srdit_residual_gate": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_int, _c_i64, _c_i64, _c_p,
@@ -236,6 +240,9 @@ def fp8_gemm(a, b, sa, sb, bias, out):
 #: epilogue flag of srdit_fp8_gemm_ex kept for old callers; it has no effect
 #: (every GEMM runs on the hand-written MFMA kernel)
 GEMM_MFMA = 0x100
+#: epilogue flag of srdit_fp8_gemm_ex: amax_out receives the largest positive
+#: output (for srdit_fp8_quant_tensor_gelu_ex) instead of max |out|
+GEMM_AMAX_POS = 0x200
 
 
 def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None):
@@ -249,6 +256,27 @@ def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None):
                                   int(sb.numel()), _ptr(bias), _ptr(out), M, N, K, out.stride(0),
                                   int(epilogue), _ptr(amax_out), _stream(a.device))
     _check(rc, "srdit_fp8_gemm_ex")
+
+
+def fp8_gemm_split(a, b, sa, sb, bias, out):
+    """a [M, K] . b [N, K]^T * sa * sb + bias with the output split into blocks:
+    ``out`` [G, M, N / G] bf16 (contiguous) receives columns [j N/G, (j+1) N/G)
+    in ``out[j]``."""
+    for name, t in (("a", a), ("b", b)):
+        if t.dtype != torch.float8_e4m3fn or t.dim() != 2 or not t.is_contiguous():
+            raise ValueError(f"fp8_gemm_split: {name} must be a contiguous 2-D float8_e4m3fn tensor")
+    M, K = a.shape
+    N = b.shape[0]
+    if b.shape[1] != K:
+        raise ValueError(f"fp8_gemm_split: inner dims differ ({K} vs {b.shape[1]})")
+    if out.dtype != torch.bfloat16 or out.dim() != 3 or not out.is_contiguous() \
+            or out.shape[1] != M or out.shape[0] * out.shape[2] != N:
+        raise ValueError(f"fp8_gemm_split: out must be contiguous bf16 [G, {M}, {N} / G]")
+    G, _, W = out.shape
+    rc = load().srdit_fp8_gemm_split(_ptr(a), _ptr(b), _ptr(sa), int(sa.numel()), _ptr(sb),
+                                     int(sb.numel()), _ptr(bias), _ptr(out), M, N, K, W, W,
+                                     M * W, _stream(a.device))
+    _check(rc, "srdit_fp8_gemm_split")
 
 
 #: capacity of the static scratch of srdit_fp8_linear_tensor_static (activation codes)
@@ -282,9 +310,11 @@ def fp8_linear_tensor_static(x, w, w_scale, bias, out):
     _check(rc, "srdit_fp8_linear_tensor_static")
 
 
-def fp8_quant_tensor_gelu(x, xq, scale, amax_ws, h=None):
+def fp8_quant_tensor_gelu(x, xq, scale, amax_ws, h=None, xmax_pos=None):
     """The per-tensor e4m3 quantisation of h = bf16(gelu_tanh(x)) into xq / scale;
-    h itself is also written when a buffer other than x is given."""
+    h itself is also written when a buffer other than x is given.  ``xmax_pos``
+    (int32 [1], nullable): the largest positive value of x as its producer wrote
+    it (``GEMM_AMAX_POS``), which lets the call skip its amax pass."""
     M, K, ldx, dt = _quant_args(x, xq)
     if dt != 0:
         raise ValueError("fp8_quant_tensor_gelu: x must be bf16")
@@ -293,10 +323,11 @@ def fp8_quant_tensor_gelu(x, xq, scale, amax_ws, h=None):
                 h.data_ptr() == x.data_ptr():
             raise ValueError("fp8_quant_tensor_gelu: h must be a bf16 buffer shaped like x "
                              "(unit column stride), not x itself")
-    rc = load().srdit_fp8_quant_tensor_gelu(_ptr(x), M, K, ldx, _ptr(h),
-                                            h.stride(0) if h is not None else 0, _ptr(xq),
-                                            _ptr(scale), _ptr(amax_ws), _stream(x.device))
-    _check(rc, "srdit_fp8_quant_tensor_gelu")
+    rc = load().srdit_fp8_quant_tensor_gelu_ex(_ptr(x), M, K, ldx, _ptr(h),
+                                               h.stride(0) if h is not None else 0, _ptr(xq),
+                                               _ptr(scale), _ptr(amax_ws), _ptr(xmax_pos),
+                                               _stream(x.device))
+    _check(rc, "srdit_fp8_quant_tensor_gelu_ex")
 
 
 def fp8_quant_apply(x, xq, scale, amax_ws):

@@ -416,11 +416,18 @@ class Block(nn.Module):
         xq, xs = quant_from(ffn_in, a0)
         if rowwise:
             hq, hs = quant_from(self.ffn[0].gemm(xq, xs, epilogue=1), None)  # GELU in the epilogue
+        elif FFN_GELU_IN_GEMM:
+            # GELU and the amax of h in the GEMM's epilogue, then the quantise pass
+            hq, hs = quant_from(self.ffn[0].gemm(xq, xs, epilogue=1, amax_out=a1), a1)
         else:
-            hlin = self.ffn[0].gemm(xq, xs)
+            # the GEMM reduces its largest positive output, which fixes the amax
+            # of GELU(x) whenever it is at least 0.375; the table call then skips
+            # its amax pass (and runs it otherwise)
+            xpos = amax[3:4]
+            hlin = self.ffn[0].gemm(xq, xs, epilogue=_lib.GEMM_AMAX_POS, amax_out=xpos)
             hq = torch.empty(hlin.shape, dtype=FP8_DTYPE, device=dev)
             hs = torch.empty(1, dtype=torch.float32, device=dev)
-            _lib.fp8_quant_tensor_gelu(hlin, hq, hs, a1)     # GELU by table, amax, quantisation
+            _lib.fp8_quant_tensor_gelu(hlin, hq, hs, a1, xmax_pos=xpos)  # GELU by table, amax, codes
         y2 = self.ffn[2].gemm(hq, hs)
         if defer:
             return x2, (y2, mod[5])
@@ -444,6 +451,14 @@ class Block(nn.Module):
 
 #: Use the fused block forward when a block's Linears are all per-tensor Fp8Linear.
 FUSED = True
+#: Per-tensor FFN: True has the first GEMM apply the GELU and reduce the amax of
+#: h in its epilogue (the same gelu_tanh and bf16 rounding as the table path, so
+#: the same codes), leaving only the quantise pass; False (the default) looks the
+#: GELU up in a table over the GEMM's bf16 output (srdit_fp8_quant_tensor_gelu).
+#: The c5 forward took 127.3-127.9 ms with True against 123.0-123.8 ms with
+#: False (interleaved in one process): tanhf in the epilogue runs while no MFMA
+#: does, the table pass runs at memory speed.
+FFN_GELU_IN_GEMM = False
 
 
 def quantize_context(context, geom, rowwise):
@@ -567,7 +582,7 @@ class SRDiT(nn.Module):
                 # (cos, sin) pairs [s, head_dim/2] for the fused RMSNorm + RoPE kernel
                 "rope_cs": torch.view_as_real(rope).reshape(f * h * w, -1).contiguous(),
                 # amax words of the per-tensor quantisers, reused in stream order
-                "amax": torch.zeros(3, dtype=torch.int32, device=device),
+                "amax": torch.zeros(4, dtype=torch.int32, device=device),
                 "amax_ctx": torch.zeros(1, dtype=torch.int32, device=device),
                 "ones": torch.ones(cfg.dim, dtype=torch.float32, device=device)}
 
@@ -641,10 +656,57 @@ class SRDiT(nn.Module):
             ctx = torch.cat([ctx, ctx.new_zeros(cfg.text_len - ctx.shape[0], ctx.shape[1])])
         return self.text_embedding(ctx.to(dt))
 
+    def _text_kv_pack(self):
+        """Every layer's cross-attention k and v weights stacked in one fp8 matrix
+        (layer by layer, k then v), their scales as one per-output-channel vector
+        and their biases as one vector, for a single split-output GEMM over the
+        context; None unless all of them are Fp8Linear of one scaling.  Built
+        once, outside stream capture, and rebuilt when a weight changes."""
+        lins = [m for blk in self.blocks for m in (blk.cross_attn.k, blk.cross_attn.v)]
+        if not lins or not all(isinstance(m, Fp8Linear) for m in lins) \
+                or len({(m.scaling, m.in_features, m.out_features) for m in lins}) != 1:
+            return None
+        key = tuple((m.weight_fp8.data_ptr(), m.weight_fp8._version, m.weight_scale.data_ptr(),
+                     m.weight_scale._version, None if m.bias is None else
+                     (m.bias.data_ptr(), m.bias._version)) for m in lins)
+        cached = self.__dict__.get("_kv_pack")
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        n = lins[0].out_features
+        w = torch.cat([m.weight_fp8 for m in lins]).contiguous()
+        sb = torch.cat([m.weight_scale.reshape(-1).float().expand(n) for m in lins]).contiguous()
+        bias = torch.cat([m.bias.to(torch.bfloat16) if m.bias is not None else
+                          torch.zeros(n, dtype=torch.bfloat16, device=w.device)
+                          for m in lins]).contiguous()
+        pack = (w, sb, bias, lins[0].scaling == "rowwise")
+        self.__dict__["_kv_pack"] = (key, pack)
+        return pack
+
     def cross_cache(self, ctx, geom):
         """Every layer's cross-attention K/V of the embedded context, computed once
         and reused by every step (WanT2VCrossAttention.init_cache, models.py:1035-1040).
-        The context is quantised once per scaling mode, not once per layer."""
+        The context is quantised once per scaling mode, not once per layer, and
+        when every layer's k and v are fp8 Linears of one scaling they run as one
+        GEMM (srdit_fp8_gemm_split): 60 projections of 512 rows each would leave
+        most CUs idle one at a time."""
+        pack = self._text_kv_pack()
+        if pack is not None:
+            w, sb, bias, rw = pack
+            cxq, cxs = quantize_context(ctx, geom, rw)
+            lc, dim = ctx.shape
+            kv = torch.empty(2 * len(self.blocks), lc, w.shape[0] // (2 * len(self.blocks)),
+                             dtype=torch.bfloat16, device=ctx.device)
+            _lib.fp8_gemm_split(cxq, w, cxs.reshape(-1), sb, bias, kv)
+            out = []
+            for i, blk in enumerate(self.blocks):
+                ca = blk.cross_attn
+                ck = torch.empty(lc, dim, dtype=torch.bfloat16, device=ctx.device)
+                _lib.rmsnorm_rope(kv[2 * i], ca.norm_k.weight, ca.norm_k.eps, None,
+                                  ca.cfg.head_dim, ck)
+                out.append((ck, kv[2 * i + 1]))
+            return out
         quantised, out = {}, []
         for blk in self.blocks:
             rw = blk.cross_attn.k.scaling == "rowwise"

@@ -195,7 +195,8 @@ int srdit_fp8_quant_tensor(const void* x, int64_t M, int64_t K, int64_t ldx, int
  * epilogue does (fp8_linear.py:238-241).
  * Runs on one hand-written MFMA kernel for every shape and scale mode (one
  * persistent workgroup per CU).  Requires K % 128 == 0, N % 16 == 0,
- * ldo % 8 == 0 and below 2^22, M*K and N*K below 2^31; a, b, out and bias
+ * ldo % 8 == 0 with (255 * ldo + N) * 2 + 16 below 2^31, M*K and N*K below
+ * 2^31; a, b, out and bias
  * 16-byte aligned, and sa / sb too when they hold one scale per row / column.
  */
 int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_rows,
@@ -211,6 +212,24 @@ int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_row
  * the output (srdit_fp8_quant_apply).  Same layout rules as srdit_fp8_gemm.
  */
 /*
+ * The scaled fp8 GEMM with its output split into column blocks: columns
+ * [j split_n, (j + 1) split_n) of out = a . b^T * sa * sb + bias go to
+ * out + j * split_stride (elements) as an [M, split_n] block with row stride
+ * ldo.  For several Linears that read one input: their weights stacked into b
+ * (and their scales into sb, their biases into bias) make one GEMM whose
+ * blocks are the separate outputs.  The refiner uses it for the text K and V
+ * of every layer, WanT2VCrossAttention.init_cache's k and v Linears over the
+ * one context (models.py:1035-1040, :1042-1062) run as per-layer
+ * Fp8Linear.forward calls in the reference (fp8_linear.py:282-297).
+ * Requires split_n % 256 == 0, N % split_n == 0, split_stride >= M * ldo and a
+ * multiple of 8; other rules as srdit_fp8_gemm.
+ */
+int srdit_fp8_gemm_split(const void* a, const void* b, const float* sa, int64_t sa_rows,
+                         const float* sb, int64_t sb_cols, const void* bias, void* out,
+                         int64_t M, int64_t N, int64_t K, int64_t ldo, int64_t split_n,
+                         int64_t split_stride, void* stream);
+
+/*
  * The FFN's hidden activation and its per-tensor e4m3 quantiser: quantises
  * h = bf16(gelu_tanh(x)) for x [M, K] bf16 (row stride ldx) as
  * srdit_fp8_quant_tensor does (same outputs, same workspace rule).  h is looked
@@ -225,10 +244,31 @@ int srdit_fp8_quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx
                                 int64_t ldh, void* xq, float* scale, uint32_t* amax_ws,
                                 void* stream);
 
+/*
+ * srdit_fp8_quant_tensor_gelu with the largest positive value of x, as the
+ * producing GEMM wrote it (srdit_fp8_gemm_ex with SRDIT_GEMM_AMAX_POS), in
+ * xmax_pos (device uint32, nullable).  When it is at least 0.375 the amax of
+ * h is the table's value there (h is non-decreasing over x >= 0 and |h| <=
+ * 0.17 below 0), so the amax pass over x is skipped; otherwise, or with h
+ * non-null, the call is srdit_fp8_quant_tensor_gelu.  Same codes and scale
+ * either way.  Replaces the same reference steps (models.py:1200-1202,
+ * fp8_linear.py:80-130).
+ */
+int srdit_fp8_quant_tensor_gelu_ex(const void* x, int64_t M, int64_t K, int64_t ldx, void* h,
+                                   int64_t ldh, void* xq, float* scale, uint32_t* amax_ws,
+                                   const uint32_t* xmax_pos, void* stream);
+
 /* Flag for the epilogue argument of srdit_fp8_gemm_ex, kept for callers that
  * still pass it: it once selected the hand-written kernel over a library path.
  * Every GEMM runs on that kernel now; the flag is accepted and has no effect. */
 #define SRDIT_GEMM_MFMA 0x100
+
+/* Flag for the epilogue argument of srdit_fp8_gemm_ex (epilogue 0 only):
+ * amax_out receives the largest positive output instead of max |out| (the
+ * float bits of a non-negative value, 0 when every output is negative, the
+ * bits of a NaN when an output is NaN).  No counterpart in the reference: it
+ * lets srdit_fp8_quant_tensor_gelu_ex skip its amax pass. */
+#define SRDIT_GEMM_AMAX_POS 0x200
 
 int srdit_fp8_gemm_ex(const void* a, const void* b, const float* sa, int64_t sa_rows,
                       const float* sb, int64_t sb_cols, const void* bias, void* out,

@@ -279,6 +279,30 @@ def test_gemm_persistent_multi_tile(M, N, K, rs, ldo):
     assert amax.item() == out2.float().abs().max().view(torch.int32).item()
 
 
+@pytest.mark.parametrize("rs", [False, True], ids=["tensor", "rowwise"])
+def test_gemm_split_output_equals_per_block_gemms(rs):
+    """Stacked weights through one split-output GEMM: each output block is bit for
+    bit the GEMM of its own weight block (512 context rows, 6 blocks of 3072)."""
+    print(f"gemm split rowwise={rs}", flush=True)
+    g = torch.Generator("cpu").manual_seed(17)
+    M, K, W, G = 512, 3072, 3072, 6
+    a = (torch.randn(M, K, generator=g) * 0.6).to(F8).cuda()
+    b = (torch.randn(G * W, K, generator=g) * 0.6).to(F8).cuda()
+    sa = (torch.rand(M, generator=g) + 0.5).cuda() if rs else torch.tensor([0.75]).cuda()
+    sb_blk = [(torch.rand(W, generator=g) / 64).cuda() if rs else torch.rand(1, generator=g).cuda()
+              for _ in range(G)]
+    sb = torch.cat([x.expand(W) for x in sb_blk]).contiguous()
+    bias = (torch.randn(G * W, generator=g)).to(torch.bfloat16).cuda()
+    out = torch.full((G, M, W), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _lib().fp8_gemm_split(a, b, sa, sb, bias, out)
+    for j in range(G):
+        ref = torch.empty(M, W, dtype=torch.bfloat16, device="cuda")
+        _lib().fp8_gemm(a, b[j * W:(j + 1) * W].contiguous(), sa, sb_blk[j].contiguous(),
+                        bias[j * W:(j + 1) * W].contiguous(), ref)
+        torch.cuda.synchronize()
+        assert torch.equal(out[j], ref), j
+
+
 def test_fp8_linear_rowwise_and_tensor():
     from sr_dit.fp8_linear import Fp8Linear
     torch.manual_seed(0)

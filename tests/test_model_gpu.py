@@ -195,6 +195,35 @@ def test_rope_fp32_matches_complex128():
     assert diff.max().item() <= 2 ** -7 * ref.float().abs().max().item()
 
 
+@pytest.mark.parametrize("scaling", ["tensor", "rowwise"])
+def test_packed_text_kv_and_gelu_epilogue_match_the_separate_paths(scaling, monkeypatch):
+    """Every layer's text K/V from one split-output GEMM equal the per-layer
+    Linears bit for bit, and the per-tensor FFN with the GELU and amax in the
+    first GEMM's epilogue equals the table path bit for bit."""
+    print(f"[case] packed text K/V and GELU epilogue, {scaling}", flush=True)
+    cfg = SMALL
+    model = mdl.build_refiner(cfg, device=DEV, scaling=scaling, seed=6, num_layers=3)
+    f, h, w = 3, 16, 16
+    geom = model.geometry(f, h, w, cfg.text_len, DEV)
+    g = torch.Generator("cpu").manual_seed(2)
+    ctx = torch.randn(cfg.text_len, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        packed = model.cross_cache(ctx, geom)
+        assert model.__dict__.get("_kv_pack") is not None
+        separate = [blk.cross_kv(ctx, geom) for blk in model.blocks]
+        torch.cuda.synchronize()
+        for (k1, v1), (k2, v2) in zip(packed, separate):
+            assert torch.equal(k1, k2) and torch.equal(v1, v2)
+        x = torch.randn(f * h * w, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+        e0 = (torch.randn(1, 6, cfg.dim, generator=g) / cfg.dim ** 0.5).to(DEV)
+        monkeypatch.setattr(mdl, "FFN_GELU_IN_GEMM", True)
+        a = model.blocks_forward(x, e0, ctx, geom)
+        monkeypatch.setattr(mdl, "FFN_GELU_IN_GEMM", False)
+        b = model.blocks_forward(x, e0, ctx, geom)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+
+
 def test_whole_30_layer_forward_graph_equals_eager():
     """The whole refiner forward at the shipped size (models.py:1877-2002): time
     and text embeddings, the patch embedding of a 48x6x90x160 latent, 30 blocks
@@ -472,3 +501,57 @@ def test_gelu_table_covers_every_bf16_value():
     assert torch.equal(h[ok].view(torch.int16), want[ok].view(torch.int16))
     print(f"[metrics] gelu table: {int(ok.sum())} finite-or-inf outputs bit-exact, "
           f"{int(nan_w.sum())} NaN", flush=True)
+
+def test_gelu_amax_shortcut_holds_over_every_bf16_value():
+    """The facts the amax shortcut rests on, over all 65,536 bf16 inputs of the
+    table: h = bf16(gelu(x)) is non-decreasing over x >= 0, and |h| below 0 stays
+    under h(0.375) (the shortcut's threshold)."""
+    from sr_dit import _lib
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = bits.reshape(128, 512).to(DEV)
+    h = torch.empty_like(x)
+    q = torch.empty(128, 512, dtype=F8, device=DEV)
+    sc = torch.empty(1, dtype=torch.float32, device=DEV)
+    ws = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _lib.fp8_quant_tensor_gelu(x, q, sc, ws, h=h)
+    xf, hf = x.float().reshape(-1), h.float().reshape(-1)
+    fin = torch.isfinite(xf)
+    pos = fin & (xf >= 0)
+    order = torch.argsort(xf[pos])
+    hp = hf[pos][order]
+    assert bool((hp[1:] >= hp[:-1]).all())
+    neg = fin & (xf < 0)
+    thr = hf[(xf == 0.375).nonzero()[0, 0]].item()
+    assert hf[neg].abs().max().item() < thr, (hf[neg].abs().max().item(), thr)
+
+
+@pytest.mark.parametrize("shift", [0.0, -30.0], ids=["shortcut", "fallback"])
+def test_gelu_amax_shortcut_gives_the_same_codes(shift):
+    """The FFN's first GEMM writing its largest positive output, then the table
+    quantiser with that word: codes and scale equal the plain call's, both when
+    the word decides the amax (shortcut) and when it does not (outputs shifted
+    below 0.375: the full amax pass runs)."""
+    from sr_dit import _lib
+    g = torch.Generator("cpu").manual_seed(21)
+    M, N, K = 2048, 2304, 512
+    a = (torch.randn(M, K, generator=g) * 0.5).to(F8).to(DEV)
+    b = (torch.randn(N, K, generator=g) * 0.5).to(F8).to(DEV)
+    sa = torch.tensor([1.0], device=DEV)
+    sb = torch.tensor([0.1], device=DEV)   # outputs ~ N(0, 0.57^2), then shifted
+    bias = torch.full((N,), shift, dtype=torch.bfloat16, device=DEV)
+    x = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    xpos = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _lib.fp8_gemm_ex(a, b, sa, sb, bias, x, epilogue=_lib.GEMM_AMAX_POS, amax_out=xpos)
+    torch.cuda.synchronize()
+    want_pos = x.float().clamp_min(0).max()
+    assert xpos.view(torch.float32).item() == want_pos.item()
+    q1, q2 = (torch.empty(M, N, dtype=F8, device=DEV) for _ in range(2))
+    s1, s2 = (torch.empty(1, dtype=torch.float32, device=DEV) for _ in range(2))
+    w1, w2 = (torch.zeros(1, dtype=torch.int32, device=DEV) for _ in range(2))
+    _lib.fp8_quant_tensor_gelu(x, q1, s1, w1)
+    _lib.fp8_quant_tensor_gelu(x, q2, s2, w2, xmax_pos=xpos)
+    torch.cuda.synchronize()
+    print(f"[metrics] largest positive output {want_pos.item():.4f}", flush=True)
+    assert (want_pos.item() >= 0.375) == (shift == 0.0)
+    assert torch.equal(w1, w2) and torch.equal(s1, s2)
+    assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8))
