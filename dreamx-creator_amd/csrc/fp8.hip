@@ -220,24 +220,6 @@ __device__ __forceinline__ i32x8_t read_frag(const uint8_t* lds, int off_lo, int
   return i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// GELU with the tanh approximation, as torch evaluates it in fp32:
-// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
-__device__ __forceinline__ float gelu_tanh(float x) {
-  const float kBeta = 0.7978845608028654f;  // sqrt(2 / pi)
-  const float kKappa = 0.044715f;
-  const float x3 = x * x * x;
-  const float inner = kBeta * (x + kKappa * x3);
-  return 0.5f * x * (1.0f + tanhf(inner));
-}
-
-// bf16 round trip (nearest even): the value torch holds after .to(bf16).
-__device__ __forceinline__ float bf16_rt(float x) {
-  typedef float f32x2v __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-  const uint32_t b = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{x, 0.f}, bf16x2v));
-  return __uint_as_float(b << 16);
-}
-
 // GELU through a table.  The FFN's hidden activation h = bf16(gelu_tanh(x)) is
 // a function of the 16 bits of a bf16 x, so the per-tensor GELU quantiser looks
 // h up in a 65,536-entry table instead of evaluating tanhf per element (the
@@ -444,7 +426,12 @@ struct GemmFrags {
 // AMAX 0: none; 1: max |out| (float bits) into *g.amax_out; 2: the largest
 // positive output instead (0 if none, and the bits of a NaN when there is one),
 // which bounds the GELU of the output (srdit_fp8_quant_tensor_gelu_ex).
-template <int EPI, int AMAX>
+//
+// BF 1: the operands are bf16 (g.K counts bytes, two per element) and the
+// scales are 1: each 32-byte fragment feeds two 32x32x16 bf16 MFMAs (its two
+// 16-byte chunks, paired the same way in both operands), which take the 64
+// cycles of the one fp8 MFMA they replace, so the data movement is unchanged.
+template <int EPI, int AMAX, int BF = 0>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fp8_gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G_LDS];
@@ -539,10 +526,25 @@ void fp8_gemm_kernel(const GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < G_NJ; ++j) acc[i][j] = f32x16_t{};
   auto mma_j = [&](const GemmFrags& f, int j) __attribute__((always_inline)) {
+    if constexpr (BF) {
 #pragma unroll
-    for (int i = 0; i < G_NI; ++i)
-      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[i], f.x[j], acc[i][j], 0,
-                                                                  0, 0, 0, 0, 0);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < G_NI; ++i) {
+          const i32x4_t wv = h ? __builtin_shufflevector(f.w[i], f.w[i], 4, 5, 6, 7)
+                               : __builtin_shufflevector(f.w[i], f.w[i], 0, 1, 2, 3);
+          const i32x4_t xv = h ? __builtin_shufflevector(f.x[j], f.x[j], 4, 5, 6, 7)
+                               : __builtin_shufflevector(f.x[j], f.x[j], 0, 1, 2, 3);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, wv), __builtin_bit_cast(bf16x8_t, xv), acc[i][j], 0,
+              0, 0);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < G_NI; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[i], f.x[j], acc[i][j], 0,
+                                                                    0, 0, 0, 0, 0);
+    }
   };
   // The MFMAs of fc, with the reads of sub-step kk of `slot` into fn between
   // them (the scheduling barriers keep that order).
@@ -592,7 +594,7 @@ void fp8_gemm_kernel(const GemmArgs g) {
     for (int j = 0; j < G_NJ; ++j) F0.x[j] = read_frag(ta + j * 32 * G_FK, roff[0][0], roff[0][1]);
   }
 
-  const float sa_t = g.sa[0], sb_t = g.sb[0];  // per-tensor scales
+  const float sa_t = BF ? 1.f : g.sa[0], sb_t = BF ? 1.f : g.sb[0];  // per-tensor scales
   int S = 0;
   for (int t = 0; t < my_tiles; ++t) {
     for (int sl = 0; sl < nks; ++sl, ++S) {
@@ -799,9 +801,15 @@ int cu_count_of_current_device() {
 int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_rows, const float* sb,
                     int64_t sb_cols, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
                     int64_t ldo, int epilogue, uint32_t* amax_out, void* stream, const char* who,
-                    int64_t split_n = 0, int64_t split_stride = 0) {
+                    int64_t split_n = 0, int64_t split_stride = 0, bool bf16 = false) {
   SRDIT_REQUIRE(a && b && sa && sb && out, "%s: null pointer", who);
   SRDIT_REQUIRE(M > 0 && N > 0 && K > 0, "%s: M, N, K must be positive", who);
+  if (bf16) {  // bf16 operands: K elements of two bytes; the kernel counts bytes
+    SRDIT_REQUIRE(K % 64 == 0 && sa_rows == 1 && sb_cols == 1 && !amax_out && !split_n,
+                  "%s: bf16 operands need K %% 64 == 0 (K=%lld), no scales, amax or split", who,
+                  (long long)K);
+    K *= 2;
+  }
   SRDIT_REQUIRE(K % 128 == 0, "%s: K=%lld must be a multiple of 128", who, (long long)K);
   SRDIT_REQUIRE(N % 16 == 0, "%s: N=%lld must be a multiple of 16", who, (long long)N);
   const int64_t width = split_n ? split_n : N;  // columns of one output block
@@ -861,7 +869,9 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
   const int64_t cus = (cu_count_of_current_device() / 8) * 8;
   const int64_t need = (tiles + 7) / 8 * 8;
   const unsigned grid = (unsigned)(cus >= 8 ? (need < cus ? need : cus) : 8);
-  if (epilogue == 0 && !amax_out) fp8_gemm_kernel<0, 0><<<grid, 512, 0, s>>>(g);
+  if (bf16 && epilogue == 0) fp8_gemm_kernel<0, 0, 1><<<grid, 512, 0, s>>>(g);
+  else if (bf16) fp8_gemm_kernel<1, 0, 1><<<grid, 512, 0, s>>>(g);
+  else if (epilogue == 0 && !amax_out) fp8_gemm_kernel<0, 0><<<grid, 512, 0, s>>>(g);
   else if (epilogue == 0 && amax_pos) fp8_gemm_kernel<0, 2><<<grid, 512, 0, s>>>(g);
   else if (epilogue == 0) fp8_gemm_kernel<0, 1><<<grid, 512, 0, s>>>(g);
   else if (!amax_out) fp8_gemm_kernel<1, 0><<<grid, 512, 0, s>>>(g);
@@ -870,6 +880,17 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
   return SRDIT_OK;
 }
 }  // namespace
+
+// The persistent GEMM on bf16 operands (contiguous rows of K elements), for
+// srdit_bf16_linear's large grids: out = bf16(a w^T + bias) [then GELU].
+int bf16_gemm_persistent(const void* a, const void* w, const void* bias, void* out, int64_t M,
+                         int64_t N, int64_t K, int64_t ldo, int gelu, void* stream,
+                         const char* who) {
+  const float* unit = static_cast<const float*>(a);  // scales are not read with bf16 operands
+  return fp8_gemm_launch(a, w, unit, 1, unit, 1, bias, out, M, N, K, ldo, gelu ? 1 : 0, nullptr,
+                         stream, who, 0, 0, true);
+}
+
 }  // namespace srdit
 
 extern "C" int srdit_fp8_gemm(const void* a, const void* b, const float* sa, int64_t sa_rows,

@@ -64,6 +64,12 @@ SIGNATURES = {
                                             _c_i64, _c_p, _c_p]),
     "srdit_rmsnorm_rope": (_c_int, [_c_p, _c_i64, _c_int, _c_i64, _c_p, _c_f, _c_p, _c_int, _c_p,
                                     _c_p]),
+    "srdit_bf16_linear": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64,
+                                   _c_i64, _c_i64, _c_int, _c_p]),
+    "srdit_linear_f32_modulated": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_int,
+                                            _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
+    "srdit_gemv_f32": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_int, _c_p, _c_i64, _c_i64,
+                                _c_i64, _c_i64, _c_p]),
     "srdit_last_error": (_c_int, [ctypes.c_char_p, _c_int]),
     "srdit_version": (_c_int, []),
     "srdit_copy_bytes": (_c_int, [_c_p, _c_p, _c_i64, _c_p]),
@@ -385,3 +391,78 @@ def rmsnorm_rope(x, w, eps, rope_cs, head_dim, out):
 def copy_bytes(src, dst, nbytes):
     rc = load().srdit_copy_bytes(_ptr(src), _ptr(dst), int(nbytes), _stream(src.device))
     _check(rc, "srdit_copy_bytes")
+
+
+# -- dense Linears at the forward's ends (csrc/dense.hip) ----------------------
+_DENSE_W_CODES = {torch.bfloat16: 0, torch.float32: 2}
+
+
+def _rows2d(name, t, dtype):
+    if t.dim() != 2 or t.stride(1) != 1 or t.dtype != dtype or not t.is_cuda:
+        raise ValueError(f"{name} must be a 2-D {dtype} device tensor with unit column stride, "
+                         f"got {t.dtype} {tuple(t.shape)} strides {t.stride()}")
+
+
+def _vec(name, t, n, dtype):
+    if t is not None and (t.dtype != dtype or t.numel() != n or not t.is_contiguous()):
+        raise ValueError(f"{name} must be a contiguous {dtype} vector of {n} values")
+
+
+def bf16_linear(a, w, bias, out, gelu=False):
+    """out [M, N] = bf16(a [M, K] @ w [N, K]^T + bias) in bf16 with fp32
+    accumulation; with ``gelu`` then bf16(gelu_tanh(out))."""
+    _rows2d("bf16_linear a", a, torch.bfloat16)
+    _rows2d("bf16_linear w", w, torch.bfloat16)
+    _rows2d("bf16_linear out", out, torch.bfloat16)
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K or tuple(out.shape) != (M, N):
+        raise ValueError(f"bf16_linear: shapes a {tuple(a.shape)} w {tuple(w.shape)} "
+                         f"out {tuple(out.shape)} disagree")
+    _vec("bf16_linear bias", bias, N, torch.bfloat16)
+    rc = load().srdit_bf16_linear(_ptr(a), a.stride(0), _ptr(w), w.stride(0), _ptr(bias),
+                                  _ptr(out), out.stride(0), M, N, K, int(bool(gelu)),
+                                  _stream(a.device))
+    _check(rc, "srdit_bf16_linear")
+
+
+def linear_f32_modulated(a, s1, m0, w, bias, out):
+    """out [M, N] fp32 = (f32(a) * s1 + m0) @ w^T + bias, a [M, K] bf16, s1/m0
+    fp32 [K], w [N, K] and bias [N] both bf16 or both fp32 (bias may be None)."""
+    _rows2d("linear_f32_modulated a", a, torch.bfloat16)
+    if w.dtype not in _DENSE_W_CODES:
+        raise ValueError(f"linear_f32_modulated: weights must be bf16 or fp32, got {w.dtype}")
+    _rows2d("linear_f32_modulated w", w, w.dtype)
+    _rows2d("linear_f32_modulated out", out, torch.float32)
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K or tuple(out.shape) != (M, N):
+        raise ValueError(f"linear_f32_modulated: shapes a {tuple(a.shape)} w {tuple(w.shape)} "
+                         f"out {tuple(out.shape)} disagree")
+    _vec("linear_f32_modulated s1", s1, K, torch.float32)
+    _vec("linear_f32_modulated m0", m0, K, torch.float32)
+    _vec("linear_f32_modulated bias", bias, N, w.dtype)
+    rc = load().srdit_linear_f32_modulated(_ptr(a), a.stride(0), _ptr(s1), _ptr(m0), _ptr(w),
+                                           w.stride(0), _ptr(bias), _DENSE_W_CODES[w.dtype],
+                                           _ptr(out), out.stride(0), M, N, K, _stream(a.device))
+    _check(rc, "srdit_linear_f32_modulated")
+
+
+def gemv_f32(x, w, bias, out):
+    """out [M, N] fp32 = x [M, K] fp32 @ w [N, K]^T + bias, w and bias both bf16 or
+    both fp32 (bias may be None); one wave per output, for a few rows."""
+    _rows2d("gemv_f32 x", x, torch.float32)
+    if w.dtype not in _DENSE_W_CODES:
+        raise ValueError(f"gemv_f32: weights must be bf16 or fp32, got {w.dtype}")
+    _rows2d("gemv_f32 w", w, w.dtype)
+    _rows2d("gemv_f32 out", out, torch.float32)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K or tuple(out.shape) != (M, N):
+        raise ValueError(f"gemv_f32: shapes x {tuple(x.shape)} w {tuple(w.shape)} "
+                         f"out {tuple(out.shape)} disagree")
+    _vec("gemv_f32 bias", bias, N, w.dtype)
+    rc = load().srdit_gemv_f32(_ptr(x), x.stride(0), _ptr(w), w.stride(0), _ptr(bias),
+                               _DENSE_W_CODES[w.dtype], _ptr(out), out.stride(0), M, N, K,
+                               _stream(x.device))
+    _check(rc, "srdit_gemv_f32")

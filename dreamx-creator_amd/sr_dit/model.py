@@ -486,9 +486,33 @@ class Head(nn.Module):
         self.modulation = nn.Parameter(torch.randn(1, 2, cfg.dim) / cfg.dim ** 0.5)
 
     def forward(self, x, e):
+        if x.is_cuda and x.dtype == torch.bfloat16:
+            return self.forward_hip(x, e)
         m = (self.modulation.float() + e.float().unsqueeze(1)).chunk(2, dim=1)
         xin = self.norm(x).float() * (1 + m[1].reshape(1, -1)) + m[0].reshape(1, -1)
         return F.linear(xin, self.head.weight.float(), self.head.bias.float())
+
+    def forward_hip(self, x, e):
+        """The same arithmetic in two kernels: the LayerNorm's bf16 output
+        (srdit_ln_modulate without modulation), then the fp32 Linear that
+        applies f32(ln) * (1 + scale) + shift to its input as it reads it
+        (srdit_linear_f32_modulated); the weights stay in their dtype (bf16 or
+        fp32), as .float() of them is exact."""
+        m = self.modulation.float() + e.float().unsqueeze(1)          # [1, 2, dim]
+        s1 = (1 + m[0, 1]).contiguous()
+        m0 = m[0, 0].contiguous()
+        xb = x.contiguous()
+        ln = torch.empty_like(xb)
+        nw, nb = self.norm.weight, self.norm.bias
+        if nw is not None:
+            nw, nb = nw.to(torch.bfloat16).contiguous(), nb.to(torch.bfloat16).contiguous()
+        _lib.ln_modulate(xb, nw, nb, None, None, self.norm.eps, ln)
+        w = self.head.weight
+        w = w if w.dtype in (torch.bfloat16, torch.float32) else w.float()
+        b = None if self.head.bias is None else self.head.bias.to(w.dtype).contiguous()
+        out = torch.empty(x.shape[0], w.shape[0], dtype=torch.float32, device=x.device)
+        _lib.linear_f32_modulated(ln, s1, m0, w.contiguous(), b, out)
+        return out
 
 
 class SRDiT(nn.Module):
@@ -591,7 +615,14 @@ class SRDiT(nn.Module):
         """t [1] -> (e [1, dim], e0 [1, 6, dim]), fp32 whatever the weights' dtype, as
         the reference's fp32 autocast region computes them (models.py:1845-1849)."""
         def lin(m, x):
-            return F.linear(x, m.weight.float(), None if m.bias is None else m.bias.float())
+            if not x.is_cuda:
+                return F.linear(x, m.weight.float(), None if m.bias is None else m.bias.float())
+            # one row: srdit_gemv_f32 reads the weights in their dtype (bf16 or fp32)
+            w = m.weight if m.weight.dtype in (torch.bfloat16, torch.float32) else m.weight.float()
+            b = None if m.bias is None else m.bias.to(w.dtype).contiguous()
+            out = torch.empty(x.shape[0], w.shape[0], dtype=torch.float32, device=x.device)
+            _lib.gemv_f32(x.float().contiguous(), w.contiguous(), b, out)
+            return out
 
         te, tp = self.time_embedding, self.time_projection
         e = lin(te[2], F.silu(lin(te[0], sinusoidal_embedding_1d(self.cfg.freq_dim, t).float())))
@@ -636,15 +667,23 @@ class SRDiT(nn.Module):
     def embed_patches(self, latent):
         """The patch-embedding Conv3d (models.py:1551-1552; kernel = stride = patch)
         as the GEMM it is: latent [C, F, ph*h, pw*w] -> tokens [F*h*w, dim] in
-        (frame, row, column) order, and the token grid.  A plain GEMM also
-        captures in a HIP graph."""
+        (frame, row, column) order, and the token grid.  On the GPU the GEMM is
+        srdit_bf16_linear (bf16 products, fp32 accumulation, the bias added
+        before the one rounding), which also captures in a HIP graph."""
         pt, ph, pw = self.cfg.patch_size
         wgt = self.patch_embedding.weight
         c, fr, hh, ww = latent.shape
         f, h, w = fr // pt, hh // ph, ww // pw
         patches = (latent.to(wgt.dtype).view(c, f, pt, h, ph, w, pw)
                    .permute(1, 3, 5, 0, 2, 4, 6).reshape(f * h * w, c * pt * ph * pw))
-        x = F.linear(patches, wgt.reshape(wgt.shape[0], -1), self.patch_embedding.bias)
+        w2 = wgt.reshape(wgt.shape[0], -1)
+        if latent.is_cuda and wgt.dtype == torch.bfloat16:
+            x = torch.empty(f * h * w, wgt.shape[0], dtype=torch.bfloat16, device=latent.device)
+            bias = self.patch_embedding.bias
+            _lib.bf16_linear(patches.contiguous(), w2.contiguous(),
+                             None if bias is None else bias.contiguous(), x)
+            return x, (f, h, w)
+        x = F.linear(patches, w2, self.patch_embedding.bias)
         return x.contiguous(), (f, h, w)
 
     def embed_text(self, context_raw):
@@ -654,6 +693,16 @@ class SRDiT(nn.Module):
         ctx = context_raw
         if ctx.shape[0] < cfg.text_len:
             ctx = torch.cat([ctx, ctx.new_zeros(cfg.text_len - ctx.shape[0], ctx.shape[1])])
+        l0, l2 = self.text_embedding[0], self.text_embedding[2]
+        if ctx.is_cuda and dt == torch.bfloat16 and l0.weight.dtype == l2.weight.dtype == dt:
+            # the two Linears, the first with the tanh GELU on its rounded output
+            # in its epilogue (srdit_bf16_linear)
+            x = ctx.to(dt).contiguous()
+            hid = torch.empty(x.shape[0], l0.weight.shape[0], dtype=dt, device=x.device)
+            _lib.bf16_linear(x, l0.weight, l0.bias, hid, gelu=True)
+            out = torch.empty(x.shape[0], l2.weight.shape[0], dtype=dt, device=x.device)
+            _lib.bf16_linear(hid, l2.weight, l2.bias, out)
+            return out
         return self.text_embedding(ctx.to(dt))
 
     def _text_kv_pack(self):

@@ -26,7 +26,7 @@ extern "C" {
 /* element type codes */
 #define SRDIT_DTYPE_BF16 0
 #define SRDIT_DTYPE_FP16 1
-#define SRDIT_DTYPE_FP32 2  /* fp8 quantiser input only */
+#define SRDIT_DTYPE_FP32 2  /* fp8 quantiser input; fp32 dense weights */
 
 /*
  * Block-grid window attention, forward.
@@ -329,6 +329,49 @@ int srdit_residual_ln_modulate(const void* x, const void* y, const float* gate, 
  */
 int srdit_rmsnorm_rope(const void* x, int64_t M, int K, int64_t ldx, const void* w, float eps,
                        const float* rope_cs, int head_dim, void* out, void* stream);
+
+/*
+ * Dense Linears at the two ends of the forward (csrc/dense.hip).  Products
+ * exact, fp32 accumulators, the bias added to the accumulator before the one
+ * rounding to the output type; only the summation order differs from torch's
+ * GEMMs on the same dtypes.  Row strides in elements; A and W rows 16-byte
+ * aligned.
+ *
+ * srdit_bf16_linear: out [M, N] = bf16(a [M, K] @ w [N, K]^T + bias [N]), all
+ * bf16 (bias may be NULL), K % 16 == 0; epilogue 1 then stores
+ * bf16(gelu_tanh(out)) of the rounded value.  Replaces the patch embedding's
+ * Conv3d with kernel = stride = patch (video_refiner/wan/modules/sr_dit/
+ * models.py:1551-1552, called at :1837) as a GEMM over the patches, and
+ * the text embedding's Linear - GELU(tanh) - Linear (models.py:1553-1556,
+ * called at :1860-1866).
+ */
+int srdit_bf16_linear(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
+                      void* out, int64_t ldo, int64_t M, int64_t N, int64_t K, int epilogue,
+                      void* stream);
+
+/*
+ * out [M, N] fp32 = xin @ w^T + bias with xin = (f32(a) * s1) + m0 rounded
+ * after the product and after the sum: a [M, K] bf16, s1 and m0 fp32 [K]
+ * (16-byte aligned), w [N, K] and bias [N] both bf16 (w_dtype
+ * SRDIT_DTYPE_BF16) or both fp32 (SRDIT_DTYPE_FP32), bias may be NULL;
+ * K % 16 == 0.  Replaces Head.forward's modulation and fp32 Linear
+ * (models.py:1372-1384) after its LayerNorm (srdit_ln_modulate with no
+ * modulation gives that LayerNorm's bf16 output).
+ */
+int srdit_linear_f32_modulated(const void* a, int64_t lda, const float* s1, const float* m0,
+                               const void* w, int64_t ldw, const void* bias, int w_dtype,
+                               float* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                               void* stream);
+
+/*
+ * out [M, N] fp32 = x [M, K] fp32 @ w [N, K]^T + bias, w and bias both bf16 or
+ * both fp32 (w_dtype), bias may be NULL; K % 8 == 0, M < 65536.  One wave per
+ * output: for the time embedding's and time projection's Linears on the
+ * one-row sinusoid (models.py:1845-1849, the fp32 region of the timestep MLP).
+ */
+int srdit_gemv_f32(const float* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                   int w_dtype, float* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                   void* stream);
 
 /* Message of the last failed call on this thread (NUL-terminated, truncated to
  * len).  Returns the message length. */

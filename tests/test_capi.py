@@ -96,3 +96,27 @@ def test_gemm_rejects_bad_layouts_without_gpu():
     assert rc == 1 and "aligned" in _lib.last_error()
     rc = lib.srdit_fp8_gemm(fake, fake, fake, 1, fake, 1, None, fake, 64, 32, 200, 32, None)
     assert rc == 1 and "K=200" in _lib.last_error()
+
+
+def test_dense_linears_reject_bad_layouts_without_gpu():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(4096)
+    # bf16 linear: K a multiple of 16, rows 16-byte aligned, epilogue 0 or 1
+    rc = lib.srdit_bf16_linear(fake, 40, fake, 40, None, fake, 64, 8, 64, 40, 0, None)
+    assert rc == 1 and "K=40" in _lib.last_error()
+    rc = lib.srdit_bf16_linear(fake, 36, fake, 32, None, fake, 64, 8, 64, 32, 0, None)
+    assert rc == 1 and "aligned" in _lib.last_error()
+    rc = lib.srdit_bf16_linear(fake, 32, fake, 32, None, fake, 64, 8, 64, 32, 2, None)
+    assert rc == 1 and "epilogue" in _lib.last_error()
+    # the modulated fp32 linear: weights bf16 or fp32, modulation vectors 16-byte aligned
+    rc = lib.srdit_linear_f32_modulated(fake, 64, fake, fake, fake, 64, None, 1, fake, 64, 8, 64,
+                                        64, None)
+    assert rc == 1 and "w_dtype" in _lib.last_error()
+    rc = lib.srdit_linear_f32_modulated(fake, 64, ctypes.c_void_p(4100), fake, fake, 64, None, 2,
+                                        fake, 64, 8, 64, 64, None)
+    assert rc == 1 and "aligned" in _lib.last_error()
+    # the GEMV: K a multiple of 8, leading dimensions cover the rows
+    rc = lib.srdit_gemv_f32(fake, 12, fake, 12, None, 0, fake, 4, 1, 4, 12, None)
+    assert rc == 1 and "K=12" in _lib.last_error()
+    rc = lib.srdit_gemv_f32(fake, 8, fake, 16, None, 0, fake, 2, 1, 4, 16, None)
+    assert rc == 1 and "leading" in _lib.last_error()
