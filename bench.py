@@ -60,6 +60,8 @@ def parse():
                          "(0: none), so the timed steps see the sustained-load clock")
     ap.add_argument("--no-comparator", action="store_true",
                     help="skip the torch gather + SDPA comparator on the GPU")
+    ap.add_argument("--no-gemm", action="store_true",
+                    help="skip the fp8 GEMM timings at the refiner's projection shapes")
     ap.add_argument("--source-hash", action="store_true",
                     help="only print the hash of the sources that decide the window kernel's traffic")
     return ap.parse_args()
@@ -416,6 +418,51 @@ def production_window(steps, warmup=3):
     return res
 
 
+def gemm_shapes(reps=20, settle_ms=60.0):
+    """The fp8 e4m3 GEMM of the refiner's projections in isolation, per-tensor scales
+    and a bf16 bias, bf16 output (srdit_fp8_gemm, the persistent MFMA kernel): the
+    21,600-token q/k/v/o and cross-attention projections (N = K = 3072) and the two
+    FFN Linears (3072 -> 14336 -> 3072).  Each shape runs untimed for settle_ms
+    first, as the window step does, then reps timed launches."""
+    import torch
+    from sr_dit import _lib
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    f8 = torch.float8_e4m3fn
+    g = torch.Generator(device=dev).manual_seed(0)
+    res = {"kernel": "fp8_gemm_kernel (persistent 256x256 tiles, LDS DMA ring)",
+           "scales": "per-tensor", "reps": reps, "peak_fp8_tflops": 5000.0}
+    for name, (M, N, K) in (("qkvo_21600x3072x3072", (21600, 3072, 3072)),
+                            ("ffn_up_21600x14336x3072", (21600, 14336, 3072)),
+                            ("ffn_down_21600x3072x14336", (21600, 3072, 14336))):
+        a = (torch.randn(M, K, generator=g, device=dev) * 2).to(f8)
+        b = (torch.randn(N, K, generator=g, device=dev) * 2).to(f8)
+        sa = torch.full((1,), 0.01, device=dev)
+        sb = torch.full((1,), 0.02, device=dev)
+        bias = torch.randn(N, generator=g, device=dev).to(torch.bfloat16)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < settle_ms:
+            for _ in range(4):
+                _lib.fp8_gemm(a, b, sa, sb, bias, out)
+            torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            _lib.fp8_gemm(a, b, sa, sb, bias, out)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        pf = 2.0 * M * N * K / (us * 1e-6) / 1e15
+        res[name] = {"us": round(us, 1), "pflops": round(pf, 3),
+                     "frac_fp8_peak": round(pf * 1e3 / 5000.0, 4)}
+        del a, b, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def gather_buckets(plan, H, W):
     """Token indices of every window of a plain plan without an anchor prefix,
     bucketed by shape: a list of ([Nw, Lq], [Nw, Lkv]) int64 CPU tensors.  Query
@@ -638,6 +685,8 @@ def main():
                 result["gpu_comparator"]["ms_per_step"] / ms, 2)
     if not args.no_prod:
         result["production_window"] = leg("production_window", production_window, 20)
+    if not args.no_gemm:
+        result["fp8_gemm"] = leg("fp8_gemm", gemm_shapes)
     if not (args.no_step and args.no_stream):
         model, build_s = build_model()
         if not args.no_step:

@@ -324,6 +324,70 @@ __global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_amax_kernel(
   }
 }
 
+// The quantise pass's walk for one wavefront.  It takes groups of 64 GQ
+// chunks, (row, base) with base a multiple of 64 GQ, row by row.  Two register
+// sets alternate, so the loads of the next group are in flight while the
+// current one is looked up, converted and stored, across row ends too.  A
+// clamped index re-reads a chunk of the row; it is not stored.  FAST: the
+// divisor's reciprocal is normal (tested once, not per element).
+constexpr int GQ = 8;  // chunks per lane per group: the table leaves one workgroup per CU
+
+template <bool FAST>
+__device__ __forceinline__ void gelu_quant_walk(const uint16_t* __restrict__ x, int64_t M,
+                                                int64_t K, int64_t ldx, const uint16_t* tab,
+                                                uint8_t* __restrict__ xq, const SharedDivisor& sd,
+                                                int64_t first_row, int64_t row_step, int lane) {
+  const int64_t nchunk = K >> 3;
+  struct Pos {
+    int64_t row, base;
+  };
+  auto advance = [&](Pos p) -> Pos {
+    p.base += 64 * GQ;
+    if (p.base >= nchunk) { p.base = 0; p.row += row_step; }
+    return p;
+  };
+  auto load = [&](Pos p, uint4 (&v)[GQ]) __attribute__((always_inline)) {
+    const uint4* xr = reinterpret_cast<const uint4*>(x + p.row * ldx);
+#pragma unroll
+    for (int u = 0; u < GQ; ++u) {
+      const int64_t c = p.base + lane + 64 * u;
+      v[u] = xr[c < nchunk ? c : nchunk - 1];
+    }
+  };
+  auto quant = [&](Pos p, const uint4 (&v)[GQ]) __attribute__((always_inline)) {
+    uint2* qr = reinterpret_cast<uint2*>(xq + p.row * K);
+#pragma unroll
+    for (int u = 0; u < GQ; ++u) {
+      const uint4 hv = lut8(tab, v[u]);
+      const uint32_t w[4] = {hv.x, hv.y, hv.z, hv.w};
+      float f[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+      const int64_t c = p.base + lane + 64 * u;
+      if (c < nchunk) qr[c] = to_e4m3x8<FAST>(f, sd);
+    }
+  };
+  Pos pa{first_row, 0};
+  if (pa.row >= M) return;
+  uint4 va[GQ], vb[GQ];
+  load(pa, va);
+  Pos pb = advance(pa);
+  if (pb.row < M) load(pb, vb);
+  while (true) {
+    quant(pa, va);
+    pa = advance(pb);
+    if (pa.row < M) load(pa, va);
+    if (pb.row >= M) break;
+    quant(pb, vb);
+    pb = advance(pa);
+    if (pb.row < M) load(pb, vb);
+    if (pa.row >= M) break;
+  }
+}
+
 __global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_quant_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
     const uint16_t* __restrict__ lut, uint8_t* __restrict__ xq, float* __restrict__ scale,
@@ -334,33 +398,10 @@ __global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_quant_kernel(
   const float s = scale_from_amax_bits(*amax_ws);
   const SharedDivisor sd(s);
   if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
-  const int64_t nchunk = K >> 3;
-  for (int64_t row = (int64_t)blockIdx.x * LUT_WAVES + wave; row < M;
-       row += (int64_t)gridDim.x * LUT_WAVES) {
-    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
-    uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
-    for (int64_t c0 = lane; c0 < nchunk; c0 += 64 * QU) {
-      uint4 v[QU];
-#pragma unroll
-      for (int u = 0; u < QU; ++u) {
-        const int64_t c = c0 + 64 * u;
-        v[u] = xr[c < nchunk ? c : nchunk - 1];
-      }
-#pragma unroll
-      for (int u = 0; u < QU; ++u) {
-        const uint4 hv = lut8(tab, v[u]);
-        const uint32_t w[4] = {hv.x, hv.y, hv.z, hv.w};
-        float f[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f[2 * i] = __uint_as_float(w[i] << 16);
-          f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-        }
-        const int64_t c = c0 + 64 * u;
-        if (c < nchunk) qr[c] = to_e4m3x8(f, sd);
-      }
-    }
-  }
+  const int64_t first = (int64_t)blockIdx.x * LUT_WAVES + wave;
+  const int64_t step = (int64_t)gridDim.x * LUT_WAVES;
+  if (sd.fast) gelu_quant_walk<true>(x, M, K, ldx, tab, xq, sd, first, step, lane);
+  else gelu_quant_walk<false>(x, M, K, ldx, tab, xq, sd, first, step, lane);
 }
 
 // ------------------------------------------------------------------ the GEMM

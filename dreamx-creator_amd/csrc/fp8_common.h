@@ -42,6 +42,10 @@ struct SharedDivisor {
   }
   __device__ __forceinline__ float div(float x) const {
     if (!fast) return x / s;
+    return div_fast(x);
+  }
+  // The quotient when `fast` holds (callers that test it once for many values).
+  __device__ __forceinline__ float div_fast(float x) const {
     const float q0 = x * r;
     const float e = __builtin_fmaf(-q0, s, x);
     return e == 0.f ? q0 : __builtin_fmaf(e, r, q0);
@@ -49,10 +53,12 @@ struct SharedDivisor {
 };
 
 // Eight values -> eight e4m3 bytes of clamp(x / s, +-448) (round to nearest even).
+// FAST: the caller has checked d.fast once for all its values.
+template <bool FAST = false>
 static __device__ __forceinline__ uint2 to_e4m3x8(const float f[8], const SharedDivisor& d) {
   float q[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = clamp_fp8(d.div(f[i]));
+  for (int i = 0; i < 8; ++i) q[i] = clamp_fp8(FAST ? d.div_fast(f[i]) : d.div(f[i]));
   int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
   lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
   int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
