@@ -437,11 +437,13 @@ __global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_quant_kernel(
 // per-wavefront LDS buffer and stored as 16 rows x 64 bytes per instruction;
 // rows past M and columns past N fall outside the store descriptor.
 //
-// Measured on one MI355X (per-tensor scales, bias, same box): 21600 x 3072 x
-// 3072 in 169-175 us (2.35-2.43 PFLOP/s), 21600 x 14336 x 3072 in 805-815 us
-// (2.33-2.36), 21600 x 3072 x 14336 in 760-790 us (2.41-2.50); without its
-// fills the same loop runs 2.85-3.3 PFLOP/s, where core-clock counters show the
-// MFMA pipe ~99% busy at the ~1.57 GHz the chip sustains under that load.
+// Measured on one MI355X (per-tensor scales, bias, random operands): 21600 x
+// 3072 x 3072 in 163-168 us (2.43-2.51 PFLOP/s), 21600 x 14336 x 3072 in
+// 795-799 us (2.38-2.39), 21600 x 3072 x 14336 in 762-763 us (2.49-2.50);
+// without its fills the same loop runs 2.85-3.3 PFLOP/s, where core-clock
+// counters show the MFMA pipe ~99% busy at the ~1.57 GHz the chip sustains
+// under that load.
+
 // Order key of the largest positive value: the float bits of a non-negative
 // x (so +inf and larger values win), 0 for negative x, and 0x7fffffff for any
 // NaN, so a NaN anywhere makes the reduced key a NaN.
