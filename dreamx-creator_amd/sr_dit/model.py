@@ -232,6 +232,42 @@ class CrossAttention(nn.Module):
         return self.o(out.view(s, n * d))
 
 
+def _fp8_pack(owner, attr, lins):
+    """Fp8Linear ``lins`` of one input stacked along their outputs, for one GEMM
+    whose output column blocks land in separate tensors (srdit_fp8_gemm_split):
+    (weights [sum N, K] e4m3, per-output-channel scales, bf16 biases (zeros
+    where a Linear has none), row-wise?).  Cached in ``owner.__dict__[attr]``
+    and rebuilt when a weight, scale or bias changes.  None unless every Linear
+    is an Fp8Linear of one scaling and shape, or while a stream is captured and
+    nothing is cached (building allocates)."""
+    if not lins or not all(isinstance(m, Fp8Linear) for m in lins) \
+            or len({(m.scaling, m.in_features, m.out_features) for m in lins}) != 1:
+        return None
+    key = tuple((m.weight_fp8.data_ptr(), m.weight_fp8._version, m.weight_scale.data_ptr(),
+                 m.weight_scale._version, None if m.bias is None else
+                 (m.bias.data_ptr(), m.bias._version)) for m in lins)
+    cached = owner.__dict__.get(attr)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    n = lins[0].out_features
+    w = torch.cat([m.weight_fp8 for m in lins]).contiguous()
+    sb = torch.cat([m.weight_scale.reshape(-1).float().expand(n) for m in lins]).contiguous()
+    bias = torch.cat([m.bias.to(torch.bfloat16) if m.bias is not None else
+                      torch.zeros(n, dtype=torch.bfloat16, device=w.device)
+                      for m in lins]).contiguous()
+    pack = (w, sb, bias, lins[0].scaling == "rowwise")
+    owner.__dict__[attr] = (key, pack)
+    return pack
+
+
+#: Self-attention q, k and v of a fused block as one split-output GEMM over the
+#: block's quantised input (q and k only where v goes to a ring or a caller's
+#: buffer); False runs three GEMMs.  Bit-identical either way.
+QKV_PACK = True
+
+
 class Block(nn.Module):
     """WanAttentionBlock, non-teacher-forcing forward (models.py:1304-1351, :1256-1262)."""
 
@@ -285,8 +321,14 @@ class Block(nn.Module):
         return (x.float() + y.float() * ep[5]).to(dt)
 
 
+    def _qkv_pack(self):
+        """This block's self-attention q, k, v as one stacked fp8 Linear
+        (``_fp8_pack``), or None."""
+        sa = self.self_attn
+        return _fp8_pack(self, "_qkv_pack_cache", [sa.q, sa.k, sa.v])
+
     def forward_fused(self, x, e, context, geom, ring=None, cross_kv=None, kv_out=None,
-                      pending=None, defer=False, kv_only=False):
+                      pending=None, defer=False, kv_only=False, mod=None):
         """The same block with the elementwise chains fused into single-pass kernels.
 
         LayerNorm + modulation (+ the amax of its output), RMSNorm + RoPE and
@@ -332,8 +374,10 @@ class Block(nn.Module):
         rowwise = sa.q.scaling == "rowwise"
         amax = geom["amax"]
         a0, a1, a2 = (None, None, None) if rowwise else (amax[0:1], amax[1:2], amax[2:3])
-        # bf16 modulation + fp32 e: one kernel computing in fp32, as .float() + e does
-        mod = (self.modulation.float() + e).reshape(6, dim).contiguous()
+        # bf16 modulation + fp32 e in fp32, as .float() + e does (``mod``: the
+        # caller computed it with every block's at once)
+        if mod is None:
+            mod = (self.modulation.float() + e).reshape(6, dim).contiguous()
 
         def quant_from(t, word):
             """e4m3 codes and scale of t: per row, or per tensor from the amax its
@@ -357,9 +401,22 @@ class Block(nn.Module):
                                       self.norm1.eps, attn_in, a0)
             x = xr
         xq, xs = quant_from(attn_in, a0)
-        q_lin = None if kv_only else sa.q.gemm(xq, xs)
-        k_lin = sa.k.gemm(xq, xs)
-        if ring is None and kv_out is not None:
+        pack = self._qkv_pack() if (QKV_PACK and not kv_only and dim % 256 == 0) else None
+        if pack is not None:
+            # q, k (and v when it goes to scratch) from one GEMM over xq
+            pw, psb, pbias, _ = pack
+            g3 = 3 if ring is None and kv_out is None else 2
+            qkv = torch.empty(g3, s, dim, dtype=bf, device=dev)
+            _lib.fp8_gemm_split(xq, pw[:g3 * dim], xs.reshape(-1), psb[:g3 * dim],
+                                pbias[:g3 * dim], qkv)
+            q_lin, k_lin = qkv[0], qkv[1]
+        else:
+            q_lin = None if kv_only else sa.q.gemm(xq, xs)
+            k_lin = sa.k.gemm(xq, xs)
+        if pack is not None and g3 == 3:
+            v = qkv[2]
+            k = torch.empty(s, dim, dtype=bf, device=dev)
+        elif ring is None and kv_out is not None:
             v = sa.v.gemm(xq, xs, out=kv_out[1])
             k = kv_out[0]
         elif ring is None:
@@ -653,16 +710,35 @@ class SRDiT(nn.Module):
             cross = self.cross_cache(context, geom)
         pending = None
         last = len(self.blocks) - 1
+        mods = self.block_mods(e0)
         for i, blk in enumerate(self.blocks):
             res = blk.forward_fused(x, e0, context, geom,
                                     ring=None if rings is None else rings[i],
                                     cross_kv=None if cross is None else cross[i],
                                     kv_out=None if kv_outs is None else kv_outs[i],
-                                    pending=pending, defer=True, kv_only=kv_only and i == last)
+                                    pending=pending, defer=True, kv_only=kv_only and i == last,
+                                    mod=None if mods is None else mods[i])
             if res is None:
                 return None
             x, pending = res
         return x if pending is None else apply_residual(x, pending)
+
+    def block_mods(self, e0):
+        """Every block's modulation + e0 in fp32 ([layers, 6, dim]), one add over the
+        blocks' stacked modulations (kept in fp32, which holds bf16 exactly, and
+        rebuilt when one changes), as each block's .float() + e computes it; None
+        while a stream is captured with nothing stacked yet."""
+        if not self.blocks:
+            return None
+        key = tuple((b.modulation.data_ptr(), b.modulation._version) for b in self.blocks)
+        cached = self.__dict__.get("_mod_stack")
+        if cached is None or cached[0] != key:
+            if torch.cuda.is_current_stream_capturing():
+                return None
+            stack = torch.cat([b.modulation.float() for b in self.blocks]).contiguous()
+            self.__dict__["_mod_stack"] = cached = (key, stack)
+        dim = self.cfg.dim
+        return (cached[1] + e0.float().reshape(1, 6, dim)).reshape(len(self.blocks), 6, dim)
 
     def embed_patches(self, latent):
         """The patch-embedding Conv3d (models.py:1551-1552; kernel = stride = patch)
@@ -709,29 +785,9 @@ class SRDiT(nn.Module):
         """Every layer's cross-attention k and v weights stacked in one fp8 matrix
         (layer by layer, k then v), their scales as one per-output-channel vector
         and their biases as one vector, for a single split-output GEMM over the
-        context; None unless all of them are Fp8Linear of one scaling.  Built
-        once, outside stream capture, and rebuilt when a weight changes."""
-        lins = [m for blk in self.blocks for m in (blk.cross_attn.k, blk.cross_attn.v)]
-        if not lins or not all(isinstance(m, Fp8Linear) for m in lins) \
-                or len({(m.scaling, m.in_features, m.out_features) for m in lins}) != 1:
-            return None
-        key = tuple((m.weight_fp8.data_ptr(), m.weight_fp8._version, m.weight_scale.data_ptr(),
-                     m.weight_scale._version, None if m.bias is None else
-                     (m.bias.data_ptr(), m.bias._version)) for m in lins)
-        cached = self.__dict__.get("_kv_pack")
-        if cached is not None and cached[0] == key:
-            return cached[1]
-        if torch.cuda.is_current_stream_capturing():
-            return None
-        n = lins[0].out_features
-        w = torch.cat([m.weight_fp8 for m in lins]).contiguous()
-        sb = torch.cat([m.weight_scale.reshape(-1).float().expand(n) for m in lins]).contiguous()
-        bias = torch.cat([m.bias.to(torch.bfloat16) if m.bias is not None else
-                          torch.zeros(n, dtype=torch.bfloat16, device=w.device)
-                          for m in lins]).contiguous()
-        pack = (w, sb, bias, lins[0].scaling == "rowwise")
-        self.__dict__["_kv_pack"] = (key, pack)
-        return pack
+        context; None unless all of them are Fp8Linear of one scaling."""
+        return _fp8_pack(self, "_kv_pack",
+                         [m for blk in self.blocks for m in (blk.cross_attn.k, blk.cross_attn.v)])
 
     def cross_cache(self, ctx, geom):
         """Every layer's cross-attention K/V of the embedded context, computed once

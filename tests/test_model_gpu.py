@@ -196,6 +196,44 @@ def test_rope_fp32_matches_complex128():
 
 
 @pytest.mark.parametrize("scaling", ["tensor", "rowwise"])
+def test_qkv_pack_and_stacked_modulations_match_the_separate_paths(scaling, monkeypatch):
+    """Each block's q, k, v from one split-output GEMM (q and k only, when K and V
+    go to caller buffers) and every block's modulation from one stacked add
+    equal the per-Linear GEMMs and per-block adds bit for bit: the block stack's
+    output and the K/V it writes."""
+    print(f"[case] packed q/k/v and stacked modulations, {scaling}", flush=True)
+    cfg = SMALL
+    model = mdl.build_refiner(cfg, device=DEV, scaling=scaling, seed=8, num_layers=3)
+    f, h, w = 3, 16, 16
+    s = f * h * w
+    geom = model.geometry(f, h, w, cfg.text_len, DEV)
+    g = torch.Generator("cpu").manual_seed(5)
+    ctx = torch.randn(cfg.text_len, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+    x = torch.randn(s, cfg.dim, generator=g).to(torch.bfloat16).to(DEV)
+    e0 = (torch.randn(1, 6, cfg.dim, generator=g) / cfg.dim ** 0.5).to(DEV)
+
+    def run():
+        out = model.blocks_forward(x, e0, ctx, geom)
+        kv = [(torch.empty(s, cfg.dim, dtype=torch.bfloat16, device=DEV),
+               torch.empty(s, cfg.dim, dtype=torch.bfloat16, device=DEV)) for _ in model.blocks]
+        out_kv = model.blocks_forward(x, e0, ctx, geom, kv_outs=kv)
+        torch.cuda.synchronize()
+        return out, out_kv, kv
+
+    with torch.no_grad():
+        a, a_kv, kv_a = run()
+        assert all(blk.__dict__.get("_qkv_pack_cache") is not None for blk in model.blocks)
+        assert model.__dict__.get("_mod_stack") is not None
+        monkeypatch.setattr(mdl, "QKV_PACK", False)
+        monkeypatch.setattr(mdl.SRDiT, "block_mods", lambda self, e0: None)
+        b, b_kv, kv_b = run()
+    assert torch.isfinite(a.float()).all()
+    assert torch.equal(a, b) and torch.equal(a_kv, b_kv)
+    for (k1, v1), (k2, v2) in zip(kv_a, kv_b):
+        assert torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
+@pytest.mark.parametrize("scaling", ["tensor", "rowwise"])
 def test_packed_text_kv_and_gelu_epilogue_match_the_separate_paths(scaling, monkeypatch):
     """Every layer's text K/V from one split-output GEMM equal the per-layer
     Linears bit for bit, and the per-tensor FFN with the GELU and amax in the
