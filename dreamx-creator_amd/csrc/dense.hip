@@ -120,19 +120,32 @@ __device__ __forceinline__ void store8<float>(float* p, const float v[8]) {
   *reinterpret_cast<f32x4_t*>(p + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
 }
 
+// The first nv (< 8, or rows not 16-byte aligned) values one at a time.
+__device__ __forceinline__ void store1(uint16_t* p, float v) { *p = f32_to_bf16_bits(v); }
+__device__ __forceinline__ void store1(float* p, float v) { *p = v; }
+
 // After the LDS tiles are written and a barrier: wave w stores its own tile's
 // 32 rows (KS = 1) or rows 8w..8w+7 of the shared tile (KS = 4).  Lane l takes
-// row l/8 of each 8-row group, columns 8 (l%8) .. +8.  N % 8 == 0, so a piece
-// is wholly inside or outside the matrix.
+// row l/8 of each 8-row group, columns 8 (l%8) .. +8, as one 16-byte store
+// where the piece is whole and the rows are 16-byte aligned (vec_out), else
+// value by value (the last piece of a row whose length is not a multiple of 8).
 template <int KS, int GELU, typename OT, typename BT>
 __device__ __forceinline__ void epilogue(const float* lds, int wave, int lane, int m_tile, int n0,
                                          int M, int N, const BT* __restrict__ bias,
-                                         OT* __restrict__ out, int64_t ldo) {
+                                         OT* __restrict__ out, int64_t ldo, bool vec_out) {
   const int c = lane & 7, rr = lane >> 3;
   const int n = n0 + 8 * c;
   if (n >= N) return;
+  const int nv = N - n < 8 ? N - n : 8;  // columns of this piece inside the matrix
   f32x8v b = {};
-  if (bias) b = load8_f32<BT>(bias + n);
+  if (bias) {
+    if (nv == 8 && (reinterpret_cast<uintptr_t>(bias) & 15) == 0) {  // uniform
+      b = load8_f32<BT>(bias + n);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b[i] = i < nv ? load1_f32<BT>(bias, n + i) : 0.f;
+    }
+  }
 #pragma unroll
   for (int q = 0; q < (KS == 1 ? 4 : 1); ++q) {
     const int r = KS == 1 ? 8 * q + rr : 8 * wave + rr;
@@ -152,7 +165,14 @@ __device__ __forceinline__ void epilogue(const float* lds, int wave, int lane, i
       v[i] += b[i];
       if (GELU) v[i] = gelu_tanh(bf16_rt(v[i]));
     }
-    store8<OT>(out + (int64_t)m * ldo + n, v);
+    OT* dst = out + (int64_t)m * ldo + n;
+    if (vec_out && nv == 8) {
+      store8<OT>(dst, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (i < nv) store1(dst + i, v[i]);
+    }
   }
 }
 
@@ -162,7 +182,7 @@ template <int GELU, int KS>
 __global__ __launch_bounds__(256) void bf16_linear_kernel(
     const uint16_t* __restrict__ a, int64_t lda, const uint16_t* __restrict__ w, int64_t ldw,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int64_t ldo, int M, int N,
-    int K) {
+    int K, bool vec_out) {
   __shared__ __attribute__((aligned(16))) float lds[4 * EPI_TILE];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m_tile = blockIdx.y * (KS == 1 ? 4 * WT_M : WT_M) + (KS == 1 ? WT_M * wave : 0);
@@ -206,7 +226,8 @@ __global__ __launch_bounds__(256) void bf16_linear_kernel(
   }
   acc_to_lds(lds + wave * EPI_TILE, c0, c1, lane);
   __syncthreads();
-  epilogue<KS, GELU, uint16_t, uint16_t>(lds, wave, lane, m_tile, n0, M, N, bias, out, ldo);
+  epilogue<KS, GELU, uint16_t, uint16_t>(lds, wave, lane, m_tile, n0, M, N, bias, out, ldo,
+                                         vec_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -269,7 +290,8 @@ template <typename WT, int KS>
 __global__ __launch_bounds__(256) void linear_f32_modulated_kernel(
     const uint16_t* __restrict__ a, int64_t lda, const float* __restrict__ s1,
     const float* __restrict__ m0, const WT* __restrict__ w, int64_t ldw,
-    const WT* __restrict__ bias, float* __restrict__ out, int64_t ldo, int M, int N, int K) {
+    const WT* __restrict__ bias, float* __restrict__ out, int64_t ldo, int M, int N, int K,
+    bool vec_out) {
   __shared__ __attribute__((aligned(16))) float lds[4 * EPI_TILE];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m_tile = blockIdx.y * (KS == 1 ? 4 * WT_M : WT_M) + (KS == 1 ? WT_M * wave : 0);
@@ -318,7 +340,7 @@ __global__ __launch_bounds__(256) void linear_f32_modulated_kernel(
   }
   acc_to_lds(lds + wave * EPI_TILE, c0, c1, lane);
   __syncthreads();
-  epilogue<KS, 0, float, WT>(lds, wave, lane, m_tile, n0, M, N, bias, out, ldo);
+  epilogue<KS, 0, float, WT>(lds, wave, lane, m_tile, n0, M, N, bias, out, ldo, vec_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -386,13 +408,14 @@ extern "C" int srdit_bf16_linear(const void* a, int64_t lda, const void* w, int6
                 "%s: bad sizes M=%lld N=%lld K=%lld", fn, (long long)M, (long long)N,
                 (long long)K);
   SRDIT_REQUIRE(K % 16 == 0, "%s: K=%lld must be a multiple of 16", fn, (long long)K);
-  SRDIT_REQUIRE(N % 8 == 0, "%s: N=%lld must be a multiple of 8", fn, (long long)N);
   SRDIT_REQUIRE(lda >= K && ldw >= K && ldo >= N, "%s: leading dimensions below the row length",
                 fn);
-  SRDIT_REQUIRE(aligned_rows16(a, lda, 2) && aligned_rows16(w, ldw, 2) &&
-                    aligned_rows16(out, ldo, 2),
-                "%s: A, W and out rows must be 16-byte aligned", fn);
-  SRDIT_REQUIRE(!bias || aligned16(bias), "%s: the bias must be 16-byte aligned", fn);
+  SRDIT_REQUIRE(aligned_rows16(a, lda, 2) && aligned_rows16(w, ldw, 2),
+                "%s: A and W rows must be 16-byte aligned", fn);
+  SRDIT_REQUIRE((reinterpret_cast<uintptr_t>(out) & 1) == 0 &&
+                    (!bias || (reinterpret_cast<uintptr_t>(bias) & 1) == 0),
+                "%s: misaligned bf16 output or bias", fn);
+  const bool vec_out = aligned_rows16(out, ldo, 2);
   SRDIT_REQUIRE(epilogue == 0 || epilogue == 1, "%s: epilogue %d is not 0 (none) or 1 (gelu)", fn,
                 epilogue);
   // Grids of at least 128 256x256 tiles with contiguous rows take the
@@ -400,6 +423,7 @@ extern "C" int srdit_bf16_linear(const void* a, int64_t lda, const void* w, int6
   // rows, like the 512-token text embedding, or odd layouts) the kernels here.
   const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
   if (big_tiles >= 128 && K % 64 == 0 && N % 16 == 0 && lda == K && ldw == K && aligned16(bias) &&
+      aligned_rows16(out, ldo, 2) &&
       M * K * 2 < (1LL << 31) && N * K * 2 < (1LL << 31) && (255 * ldo + N) * 2 + 16 < (1LL << 31))
     return bf16_gemm_persistent(a, w, bias, out, M, N, K, ldo, epilogue, stream, fn);
   const int ks = pick_ks(M, N, K);
@@ -410,8 +434,9 @@ extern "C" int srdit_bf16_linear(const void* a, int64_t lda, const void* w, int6
   const uint16_t* wp = static_cast<const uint16_t*>(w);
   const uint16_t* bp = static_cast<const uint16_t*>(bias);
   uint16_t* op = static_cast<uint16_t*>(out);
-#define SRDIT_BL(G, KS) \
-  bf16_linear_kernel<G, KS><<<grid, 256, 0, s>>>(ap, lda, wp, ldw, bp, op, ldo, (int)M, (int)N, (int)K)
+#define SRDIT_BL(G, KS)                                                                      \
+  bf16_linear_kernel<G, KS><<<grid, 256, 0, s>>>(ap, lda, wp, ldw, bp, op, ldo, (int)M, (int)N, \
+                                                 (int)K, vec_out)
   if (epilogue && ks == 4) SRDIT_BL(1, 4);
   else if (epilogue) SRDIT_BL(1, 1);
   else if (ks == 4) SRDIT_BL(0, 4);
@@ -433,14 +458,16 @@ extern "C" int srdit_linear_f32_modulated(const void* a, int64_t lda, const floa
                 "%s: bad sizes M=%lld N=%lld K=%lld", fn, (long long)M, (long long)N,
                 (long long)K);
   SRDIT_REQUIRE(K % 16 == 0, "%s: K=%lld must be a multiple of 16", fn, (long long)K);
-  SRDIT_REQUIRE(N % 8 == 0, "%s: N=%lld must be a multiple of 8", fn, (long long)N);
   SRDIT_REQUIRE(lda >= K && ldw >= K && ldo >= N, "%s: leading dimensions below the row length",
                 fn);
   const int welem = w_dtype == SRDIT_DTYPE_FP32 ? 4 : 2;
-  SRDIT_REQUIRE(aligned_rows16(a, lda, 2) && aligned_rows16(w, ldw, welem) &&
-                    aligned_rows16(out, ldo, 4) && aligned16(s1) && aligned16(m0),
-                "%s: A, W, out, s1 and m0 must be 16-byte aligned (rows included)", fn);
-  SRDIT_REQUIRE(!bias || aligned16(bias), "%s: the bias must be 16-byte aligned", fn);
+  SRDIT_REQUIRE(aligned_rows16(a, lda, 2) && aligned_rows16(w, ldw, welem) && aligned16(s1) &&
+                    aligned16(m0),
+                "%s: A, W, s1 and m0 must be 16-byte aligned (rows included)", fn);
+  SRDIT_REQUIRE((reinterpret_cast<uintptr_t>(out) & 3) == 0 &&
+                    (!bias || (reinterpret_cast<uintptr_t>(bias) & (welem - 1)) == 0),
+                "%s: misaligned output or bias", fn);
+  const bool vec_out = aligned_rows16(out, ldo, 4);
   const int ks = pick_ks(M, N, K);
   const dim3 grid = dense_grid(M, N, ks);
   SRDIT_REQUIRE(grid.y < 65536u * 16, "%s: M=%lld too large", fn, (long long)M);
@@ -450,7 +477,7 @@ extern "C" int srdit_linear_f32_modulated(const void* a, int64_t lda, const floa
   linear_f32_modulated_kernel<WT, KS><<<grid, 256, 0, s>>>(ap, lda, s1, m0,                     \
                                                            static_cast<const WT*>(w), ldw,      \
                                                            static_cast<const WT*>(bias), out,   \
-                                                           ldo, (int)M, (int)N, (int)K)
+                                                           ldo, (int)M, (int)N, (int)K, vec_out)
   if (w_dtype == SRDIT_DTYPE_FP32 && ks == 4) SRDIT_LF(float, 4);
   else if (w_dtype == SRDIT_DTYPE_FP32) SRDIT_LF(float, 1);
   else if (ks == 4) SRDIT_LF(uint16_t, 4);

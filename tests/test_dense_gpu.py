@@ -30,7 +30,8 @@ def _gelu64(x):
 
 @pytest.mark.parametrize("M,N,K,gelu", [(1000, 384, 64, False), (512, 256, 4096, True),
                                         (3000, 3072, 64, False), (2100, 4096, 128, True),
-                                        (77, 200, 48, False), (130, 96, 32, True)])
+                                        (77, 200, 48, False), (130, 96, 32, True),
+                                        (50, 37, 32, True), (300, 1027, 64, False)])
 def test_bf16_linear_matches_float64(M, N, K, gelu):
     print(f"[case] bf16_linear M={M} N={N} K={K} gelu={gelu}", flush=True)
     g = torch.Generator("cpu").manual_seed(M + N + K)
@@ -62,7 +63,7 @@ def test_bf16_linear_matches_float64(M, N, K, gelu):
 
 
 @pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32], ids=["w_bf16", "w_fp32"])
-@pytest.mark.parametrize("M,N,K", [(1000, 64, 3072), (70, 40, 80)])
+@pytest.mark.parametrize("M,N,K", [(1000, 64, 3072), (70, 40, 80), (33, 13, 48)])
 def test_linear_f32_modulated_matches_float64(M, N, K, wdt):
     print(f"[case] linear_f32_modulated M={M} N={N} K={K} w={wdt}", flush=True)
     g = torch.Generator("cpu").manual_seed(M * 7 + K)
