@@ -263,7 +263,7 @@ def _fp8_pack(owner, attr, lins):
 
 
 #: Self-attention q, k and v of a fused block as one split-output GEMM over the
-#: block's quantised input (q and k only where v goes to a ring or a caller's
+#: block's quantised input (V then copied where it goes: a ring or a caller's
 #: buffer); False runs three GEMMs.  Bit-identical either way.
 QKV_PACK = True
 
@@ -403,28 +403,32 @@ class Block(nn.Module):
         xq, xs = quant_from(attn_in, a0)
         pack = self._qkv_pack() if (QKV_PACK and not kv_only and dim % 256 == 0) else None
         if pack is not None:
-            # q, k (and v when it goes to scratch) from one GEMM over xq
+            # q, k and v from one GEMM over xq; V is then copied to its ring region
+            # or the caller's buffer (a 16-byte copy costs less than the GEMM round
+            # a separate V GEMM adds at 10,800 rows)
             pw, psb, pbias, _ = pack
-            g3 = 3 if ring is None and kv_out is None else 2
-            qkv = torch.empty(g3, s, dim, dtype=bf, device=dev)
-            _lib.fp8_gemm_split(xq, pw[:g3 * dim], xs.reshape(-1), psb[:g3 * dim],
-                                pbias[:g3 * dim], qkv)
-            q_lin, k_lin = qkv[0], qkv[1]
+            qkv = torch.empty(3, s, dim, dtype=bf, device=dev)
+            _lib.fp8_gemm_split(xq, pw, xs.reshape(-1), psb, pbias, qkv)
+            q_lin, k_lin, v = qkv[0], qkv[1], qkv[2]
+            if ring is None and kv_out is None:
+                k = torch.empty(s, dim, dtype=bf, device=dev)
+            else:
+                vdst = kv_out[1] if ring is None else ring.current_v(0, f).view(s, dim)
+                k = kv_out[0] if ring is None else ring.current_k(0, f).view(s, dim)
+                _lib.copy_bytes(v, vdst, v.numel() * v.element_size())
+                v = vdst
         else:
             q_lin = None if kv_only else sa.q.gemm(xq, xs)
             k_lin = sa.k.gemm(xq, xs)
-        if pack is not None and g3 == 3:
-            v = qkv[2]
-            k = torch.empty(s, dim, dtype=bf, device=dev)
-        elif ring is None and kv_out is not None:
-            v = sa.v.gemm(xq, xs, out=kv_out[1])
-            k = kv_out[0]
-        elif ring is None:
-            v = sa.v.gemm(xq, xs)
-            k = torch.empty(s, dim, dtype=bf, device=dev)
-        else:
-            v = sa.v.gemm(xq, xs, out=ring.current_v(0, f).view(s, dim))
-            k = ring.current_k(0, f).view(s, dim)
+            if ring is None and kv_out is not None:
+                v = sa.v.gemm(xq, xs, out=kv_out[1])
+                k = kv_out[0]
+            elif ring is None:
+                v = sa.v.gemm(xq, xs)
+                k = torch.empty(s, dim, dtype=bf, device=dev)
+            else:
+                v = sa.v.gemm(xq, xs, out=ring.current_v(0, f).view(s, dim))
+                k = ring.current_k(0, f).view(s, dim)
         _lib.rmsnorm_rope(k_lin, sa.norm_k.weight, sa.norm_k.eps, geom["rope_cs"], d, k)
         if kv_only:
             return None
