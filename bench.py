@@ -264,8 +264,9 @@ def refiner_step(model, build_s, replays, warmup):
         ev[0][1].record(stream)
         torch.cuda.synchronize()
         eager_ms = ev[0][0].elapsed_time(ev[0][1])
+        from sr_dit import _lib
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with torch.cuda.graph(graph, stream=_lib.capture_stream(dev)):
             y = fwd()
         graph.replay()
         torch.cuda.synchronize()

@@ -202,7 +202,21 @@ struct GemmArgs {
   // Split output (0: none): columns [j split_n, (j + 1) split_n) are stored at
   // out + j split_stride as a block of rows of stride ldo.
   int64_t split_n, split_stride;
+  // This launch's tiles: [task_base, task_base + n_tasks) of the raster order.
+  int task_base, n_tasks;
+  // split_k > 0: each of those tiles is split over split_k workgroups along K.
+  // Workgroup u takes tile task_base + u / split_k and the K stages
+  // [c nks / split_k, (c + 1) nks / split_k), c = u % split_k, and writes its fp32
+  // partial to ws_part; the last of a tile's workgroups to arrive (ws_cnt, one
+  // word per tile, left 0) sums the partials in chunk order and stores the tile.
+  int split_k;
+  float* ws_part;
+  uint32_t* ws_cnt;
 };
+
+// Bytes of one split-K partial, a 256 x 256 fp32 tile: 8 wavefronts x 8 accumulator
+// blocks x 16 registers x 64 lanes.
+constexpr int64_t G_PART_BYTES = 8 * 8 * 16 * 64 * 4;
 
 __device__ __forceinline__ void compiler_fence_gemm() { asm volatile("" ::: "memory"); }
 
@@ -474,7 +488,7 @@ struct GemmFrags {
 // scales are 1: each 32-byte fragment feeds two 32x32x16 bf16 MFMAs (its two
 // 16-byte chunks, paired the same way in both operands), which take the 64
 // cycles of the one fp8 MFMA they replace, so the data movement is unchanged.
-template <int EPI, int AMAX, int BF = 0>
+template <int EPI, int AMAX, int BF = 0, bool SPLIT = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fp8_gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G_LDS];
@@ -482,17 +496,25 @@ void fp8_gemm_kernel(const GemmArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave & 1, wn = wave >> 1;
 
-  const uint32_t n_tasks = (uint32_t)g.tiles_m * g.tiles_n;
+  const uint32_t n_tasks = (uint32_t)g.n_tasks;
+  constexpr bool splitk = SPLIT;  // the split launch: one K chunk of one tile per workgroup
   const uint32_t xcd = blockIdx.x & 7u, wslot = blockIdx.x >> 3, per = gridDim.x >> 3;
   const uint32_t r0 = xcd * (n_tasks >> 3) + min(xcd, n_tasks & 7u);
   const uint32_t r1 = r0 + (n_tasks >> 3) + (xcd < (n_tasks & 7u) ? 1u : 0u);
-  const int my_tiles = (r0 + wslot < r1) ? (int)((r1 - r0 - wslot + per - 1) / per) : 0;
+  // split-K: one unit per workgroup (tile sk_tile of the launch, K chunk sk_c)
+  const int unit = (int)blockIdx.x;
+  const int sk_tile = splitk ? unit / g.split_k : 0, sk_c = splitk ? unit % g.split_k : 0;
+  const int my_tiles = splitk ? (sk_tile < (int)n_tasks ? 1 : 0)
+                              : ((r0 + wslot < r1) ? (int)((r1 - r0 - wslot + per - 1) / per) : 0);
   if (my_tiles == 0) return;
-  const int nks = g.K / G_FK;  // stages per tile
+  const int nks_tile = g.K / G_FK;  // stages of a whole tile
+  const int k_first = splitk ? sk_c * nks_tile / g.split_k : 0;
+  const int nks = splitk ? (sk_c + 1) * nks_tile / g.split_k - k_first : nks_tile;  // per task
   const int n_total = my_tiles * nks;
   const int width = G_GROUP_M * g.tiles_n;
   auto coords = [&](int t, int& m0, int& n0) __attribute__((always_inline)) {
-    const uint32_t task = r0 + wslot + per * (uint32_t)t;
+    const uint32_t task = (uint32_t)g.task_base +
+                          (splitk ? (uint32_t)sk_tile : r0 + wslot + per * (uint32_t)t);
     const int group = task / width;
     const int first_m = group * G_GROUP_M;
     const int gsize = min(g.tiles_m - first_m, G_GROUP_M);
@@ -540,7 +562,7 @@ void fp8_gemm_kernel(const GemmArgs g) {
       f_rb = rsrc_of(g.b + (int64_t)n0 * g.K, (int64_t)(g.N - n0) * g.K);
     }
     const uint32_t base = lds_w + f_slot * G_SLOT;
-    const int koff = f_kt * G_FK;
+    const int koff = (k_first + f_kt) * G_FK;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       dma(f_ra, ((q & 1) ? fv_odd : fv_even) + q * frow8, koff, base + q * 1024);
@@ -655,6 +677,59 @@ void fp8_gemm_kernel(const GemmArgs g) {
     }
 
     // ---- epilogue of tile t
+    if constexpr (SPLIT) {  // publish this K chunk; the tile's last arrival stores it
+      waitcnt_vm<0>();
+      // accumulator register 4 r4 + e of block (i, j), lane l: float
+      // (((w 8 + i G_NJ + j) 4 + r4) 64 + l) 4 + e of the unit's partial
+      auto part_of = [&](int u) __attribute__((always_inline)) {
+        return g.ws_part + (int64_t)u * (G_PART_BYTES / 4) + (int64_t)wave * (8 * 16 * 64);
+      };
+      float* wp = part_of(unit);
+#pragma unroll
+      for (int i = 0; i < G_NI; ++i)
+#pragma unroll
+        for (int j = 0; j < G_NJ; ++j)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4)
+            *reinterpret_cast<f32x4_t*>(wp + (((i * G_NJ + j) * 4 + r4) * 64 + lane) * 4) =
+                f32x4_t{acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2],
+                        acc[i][j][4 * r4 + 3]};
+      __threadfence();  // release: the partial is visible to every XCD
+      __syncthreads();
+      // epilogue-data region 1 is unused with one task per workgroup
+      uint32_t* arrivals = reinterpret_cast<uint32_t*>(smem + G_EPI_OFF + G_EPI_REG);
+      if (threadIdx.x == 0) *arrivals = atomicAdd(g.ws_cnt + sk_tile, 1u);
+      __syncthreads();
+      if (*arrivals != (uint32_t)(g.split_k - 1)) return;  // uniform: not the last arrival
+      __threadfence();  // acquire: the other chunks' partials
+      // the tile's sum, chunk by chunk in K order (this chunk's own partial
+      // included), so the result does not depend on the order of arrival
+      for (int c = 0; c < g.split_k; ++c) {
+        const float* rp = part_of(sk_tile * g.split_k + c);
+#pragma unroll
+        for (int i = 0; i < G_NI; ++i) {
+          // one accumulator row of blocks at a time (32 registers of loads in
+          // flight, not the whole partial's 128)
+          f32x4_t v[G_NJ][4];
+#pragma unroll
+          for (int j = 0; j < G_NJ; ++j)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+              v[j][r4] = *reinterpret_cast<const f32x4_t*>(
+                  rp + (((i * G_NJ + j) * 4 + r4) * 64 + lane) * 4);
+#pragma unroll
+          for (int j = 0; j < G_NJ; ++j)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                acc[i][j][4 * r4 + e] = c == 0 ? v[j][r4][e] : acc[i][j][4 * r4 + e] + v[j][r4][e];
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      if (threadIdx.x == 0)  // ready for the next launch
+        __hip_atomic_store(g.ws_cnt + sk_tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     int m0, n0;
     coords(t, m0, n0);
     const int rows = min(GT, g.M - m0);
@@ -841,10 +916,47 @@ int cu_count_of_current_device() {
   return cache[dev];
 }
 
+// Split-K of a GEMM's last, partial round of tiles.  With T tiles on G
+// workgroups the persistent launch takes ceil(T / G) rounds of a whole tile's K
+// stages even when the last round holds a few tiles (10800 x 3072 x 14336: 516
+// tiles, two rounds and 4 tiles on 256 CUs).  Those tail = T mod G tiles can go
+// to a second launch instead, each split over S workgroups along K.  Measured on
+// MI355X, in K stages of a lightly loaded chip (about 1 us each): the last
+// round costs nks stages unsplit, and a split tile about ceil(nks / S) + 5
+// (launch, partial store, epilogue) + 4 S (the last arrival reads S partials of
+// 256 KB back, latency-bound at one workgroup).  So only long K pays
+// (10800 x 3072 x 14336: 475 -> 408 us; at K = 3072 the split is slower), and
+// only a small tail: 208 workgroups storing and re-reading partials at once
+// made a 104-tile tail slower than its unsplit round.
+struct TailSplit {
+  int tail = 0, split = 0;  // split == 0: one launch over every tile
+};
+
+TailSplit plan_tail_split(int64_t tiles, int64_t grid, int nks, int64_t max_units) {
+  TailSplit p;
+  const int64_t tail = tiles % grid;
+  if (tiles < grid || tail == 0 || 8 * tail > grid) return p;
+  double best = 0.75 * nks;  // split only when it saves a quarter of the round
+  for (int S = 2; S <= nks && tail * S <= grid && tail * S <= max_units; ++S) {
+    const double cost = (double)((nks + S - 1) / S) + 5.0 + 4.0 * S;
+    if (cost < best) {
+      best = cost;
+      p.tail = (int)tail;
+      p.split = S;
+    }
+  }
+  return p;
+}
+
+// Split-K workspace: one arrival counter per tail tile (left 0 by every
+// launch), then the partials, G_PART_BYTES per workgroup of the split launch.
+constexpr int64_t WS_COUNTERS = 4096;
+
 int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_rows, const float* sb,
                     int64_t sb_cols, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
                     int64_t ldo, int epilogue, uint32_t* amax_out, void* stream, const char* who,
-                    int64_t split_n = 0, int64_t split_stride = 0, bool bf16 = false) {
+                    int64_t split_n = 0, int64_t split_stride = 0, bool bf16 = false,
+                    void* workspace = nullptr, int64_t workspace_bytes = 0) {
   SRDIT_REQUIRE(a && b && sa && sb && out, "%s: null pointer", who);
   SRDIT_REQUIRE(M > 0 && N > 0 && K > 0, "%s: M, N, K must be positive", who);
   if (bf16) {  // bf16 operands: K elements of two bytes; the kernel counts bytes
@@ -903,6 +1015,8 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
   g.split_stride = split_stride;
   const int64_t tiles = (int64_t)g.tiles_m * g.tiles_n;
   SRDIT_REQUIRE(tiles < (int64_t(1) << 31), "%s: too many tiles", who);
+  SRDIT_REQUIRE(!workspace || (aligned16(workspace) && workspace_bytes >= 0),
+                "%s: the workspace must be 16-byte aligned", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (amax_out) {
     clear_u32_kernel<<<1, 1, 0, s>>>(amax_out);
@@ -911,15 +1025,39 @@ int fp8_gemm_launch(const void* a, const void* b, const float* sa, int64_t sa_ro
   // one workgroup per CU, a multiple of 8 (one share per XCD), no more than the tiles need
   const int64_t cus = (cu_count_of_current_device() / 8) * 8;
   const int64_t need = (tiles + 7) / 8 * 8;
-  const unsigned grid = (unsigned)(cus >= 8 ? (need < cus ? need : cus) : 8);
-  if (bf16 && epilogue == 0) fp8_gemm_kernel<0, 0, 1><<<grid, 512, 0, s>>>(g);
-  else if (bf16) fp8_gemm_kernel<1, 0, 1><<<grid, 512, 0, s>>>(g);
-  else if (epilogue == 0 && !amax_out) fp8_gemm_kernel<0, 0><<<grid, 512, 0, s>>>(g);
-  else if (epilogue == 0 && amax_pos) fp8_gemm_kernel<0, 2><<<grid, 512, 0, s>>>(g);
-  else if (epilogue == 0) fp8_gemm_kernel<0, 1><<<grid, 512, 0, s>>>(g);
-  else if (!amax_out) fp8_gemm_kernel<1, 0><<<grid, 512, 0, s>>>(g);
-  else fp8_gemm_kernel<1, 1><<<grid, 512, 0, s>>>(g);
+  unsigned grid = (unsigned)(cus >= 8 ? (need < cus ? need : cus) : 8);
+  const int64_t max_units =
+      workspace && workspace_bytes > WS_COUNTERS ? (workspace_bytes - WS_COUNTERS) / G_PART_BYTES : 0;
+  const TailSplit ts = max_units >= 2 && !bf16
+                           ? plan_tail_split(tiles, grid, g.K / G_FK, max_units)
+                           : TailSplit{};
+  auto launch = [&](const GemmArgs& ga, unsigned nwg, auto split_c) {
+    constexpr bool SP = decltype(split_c)::value;
+    if (bf16 && epilogue == 0) fp8_gemm_kernel<0, 0, 1><<<nwg, 512, 0, s>>>(ga);
+    else if (bf16) fp8_gemm_kernel<1, 0, 1><<<nwg, 512, 0, s>>>(ga);
+    else if (epilogue == 0 && !amax_out) fp8_gemm_kernel<0, 0, 0, SP><<<nwg, 512, 0, s>>>(ga);
+    else if (epilogue == 0 && amax_pos) fp8_gemm_kernel<0, 2, 0, SP><<<nwg, 512, 0, s>>>(ga);
+    else if (epilogue == 0) fp8_gemm_kernel<0, 1, 0, SP><<<nwg, 512, 0, s>>>(ga);
+    else if (!amax_out) fp8_gemm_kernel<1, 0, 0, SP><<<nwg, 512, 0, s>>>(ga);
+    else fp8_gemm_kernel<1, 1, 0, SP><<<nwg, 512, 0, s>>>(ga);
+  };
+  // the whole rounds (every tile when nothing is split)
+  g.task_base = 0;
+  g.n_tasks = (int)(tiles - ts.tail);
+  g.split_k = 0;
+  g.ws_part = nullptr;
+  g.ws_cnt = nullptr;
+  launch(g, grid, std::false_type{});
   SRDIT_LAUNCH_CHECK("fp8_gemm_kernel");
+  if (ts.split) {  // the last round's tiles, split along K
+    g.task_base = g.n_tasks;
+    g.n_tasks = ts.tail;
+    g.split_k = ts.split;
+    g.ws_cnt = static_cast<uint32_t*>(workspace);
+    g.ws_part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + WS_COUNTERS);
+    launch(g, (unsigned)(ts.tail * ts.split), std::true_type{});
+    SRDIT_LAUNCH_CHECK("fp8_gemm_kernel (split tail)");
+  }
   return SRDIT_OK;
 }
 }  // namespace
@@ -959,6 +1097,18 @@ extern "C" int srdit_fp8_gemm_split(const void* a, const void* b, const float* s
                 (long long)split_n);
   return fp8_gemm_launch(a, b, sa, sa_rows, sb, sb_cols, bias, out, M, N, K, ldo, 0, nullptr,
                          stream, "srdit_fp8_gemm_split", split_n, split_stride);
+}
+
+extern "C" int srdit_fp8_gemm_ws(const void* a, const void* b, const float* sa, int64_t sa_rows,
+                                 const float* sb, int64_t sb_cols, const void* bias, void* out,
+                                 int64_t M, int64_t N, int64_t K, int64_t ldo, int epilogue,
+                                 uint32_t* amax_out, int64_t split_n, int64_t split_stride,
+                                 void* workspace, int64_t workspace_bytes, void* stream) {
+  SRDIT_REQUIRE(split_n >= 0, "srdit_fp8_gemm_ws: split_n=%lld must not be negative",
+                (long long)split_n);
+  return fp8_gemm_launch(a, b, sa, sa_rows, sb, sb_cols, bias, out, M, N, K, ldo, epilogue,
+                         amax_out, stream, "srdit_fp8_gemm_ws", split_n, split_stride, false,
+                         workspace, workspace_bytes);
 }
 
 extern "C" int srdit_fp8_quant_apply(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype,

@@ -49,6 +49,9 @@ SIGNATURES = {
                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p]),
     "srdit_fp8_gemm_split": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p,
                                       _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p]),
+    "srdit_fp8_gemm_ws": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p,
+                                   _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_i64,
+                                   _c_p, _c_i64, _c_p]),
     "srdit_fp8_quant_apply": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
                                        _c_p]),
     "srdit_fp8_quant_tensor_gelu": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p,
@@ -251,23 +254,83 @@ GEMM_MFMA = 0x100
 GEMM_AMAX_POS = 0x200
 
 
-def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None):
+#: bytes of a split-K workspace of srdit_fp8_gemm_ws (SRDIT_GEMM_WS_BYTES)
+GEMM_WS_BYTES = 4096 + 256 * 262144
+_GEMM_WS = {}
+
+
+def gemm_workspace(device, stream=None):
+    """The split-K workspace of srdit_fp8_gemm_ws for ``stream`` (default: the
+    current stream of ``device``): GEMM_WS_BYTES of device memory whose first
+    4096 bytes (the arrival counters) are zeroed once, kept for the stream.  None
+    while that stream is captured and has none yet (a graph must not own it):
+    its GEMMs then run unsplit.  ``capture_stream`` gives a stream that has one."""
+    device = torch.device(device)
+    if device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    s = stream if stream is not None else torch.cuda.current_stream(device)
+    key = (device.index, s.cuda_stream)
+    ws = _GEMM_WS.get(key)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        with torch.cuda.stream(s):
+            ws = torch.empty(GEMM_WS_BYTES, dtype=torch.uint8, device=device)
+            ws[:4096].zero_()
+        _GEMM_WS[key] = ws
+    return ws
+
+
+_CAPTURE_STREAMS = {}
+
+
+def capture_stream(device):
+    """A side stream of ``device`` for graph capture (torch.cuda.graph(...,
+    stream=)), one per device, whose GEMM workspace exists before the capture."""
+    device = torch.device(device)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    s = _CAPTURE_STREAMS.get(idx)
+    if s is None:
+        s = _CAPTURE_STREAMS[idx] = torch.cuda.Stream(torch.device("cuda", idx))
+        gemm_workspace(torch.device("cuda", idx), s)
+        s.synchronize()
+    return s
+
+
+def _gemm_ws(a, out, M, N, K, ldo, epilogue, amax_out, split_n, split_stride, sa, sb, bias, b,
+             who):
+    ws = gemm_workspace(a.device)
+    rc = load().srdit_fp8_gemm_ws(_ptr(a), _ptr(b), _ptr(sa), int(sa.numel()), _ptr(sb),
+                                  int(sb.numel()), _ptr(bias), _ptr(out), M, N, K, ldo,
+                                  int(epilogue), _ptr(amax_out), split_n, split_stride,
+                                  _ptr(ws), 0 if ws is None else ws.numel(), _stream(a.device))
+    _check(rc, who)
+
+
+def fp8_gemm_ex(a, b, sa, sb, bias, out, *, epilogue=0, amax_out=None, split_tail=True):
     """fp8_gemm with an epilogue (0 none, 1 GELU-tanh) and an optional amax word
-    (cleared by the call, then the bits of max |out|)."""
+    (cleared by the call, then the bits of max |out|).  ``split_tail``: a last
+    round of tiles less than half full runs split along K (srdit_fp8_gemm_ws,
+    with this stream's workspace); the results differ from the unsplit GEMM's
+    only in the fp32 summation order."""
     M, K = a.shape
     N = b.shape[0]
     if out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
         raise ValueError(f"fp8_gemm_ex: out must be bf16 [{M}, {N}] with unit column stride")
+    if split_tail:
+        _gemm_ws(a, out, M, N, K, out.stride(0), epilogue, amax_out, 0, 0, sa, sb, bias, b,
+                 "srdit_fp8_gemm_ws")
+        return
     rc = load().srdit_fp8_gemm_ex(_ptr(a), _ptr(b), _ptr(sa), int(sa.numel()), _ptr(sb),
                                   int(sb.numel()), _ptr(bias), _ptr(out), M, N, K, out.stride(0),
                                   int(epilogue), _ptr(amax_out), _stream(a.device))
     _check(rc, "srdit_fp8_gemm_ex")
 
 
-def fp8_gemm_split(a, b, sa, sb, bias, out):
+def fp8_gemm_split(a, b, sa, sb, bias, out, *, split_tail=True):
     """a [M, K] . b [N, K]^T * sa * sb + bias with the output split into blocks:
     ``out`` [G, M, N / G] bf16 (contiguous) receives columns [j N/G, (j+1) N/G)
-    in ``out[j]``."""
+    in ``out[j]``.  ``split_tail`` as fp8_gemm_ex."""
     for name, t in (("a", a), ("b", b)):
         if t.dtype != torch.float8_e4m3fn or t.dim() != 2 or not t.is_contiguous():
             raise ValueError(f"fp8_gemm_split: {name} must be a contiguous 2-D float8_e4m3fn tensor")
@@ -279,6 +342,9 @@ def fp8_gemm_split(a, b, sa, sb, bias, out):
             or out.shape[1] != M or out.shape[0] * out.shape[2] != N:
         raise ValueError(f"fp8_gemm_split: out must be contiguous bf16 [G, {M}, {N} / G]")
     G, _, W = out.shape
+    if split_tail:
+        _gemm_ws(a, out, M, N, K, W, 0, None, W, M * W, sa, sb, bias, b, "srdit_fp8_gemm_ws")
+        return
     rc = load().srdit_fp8_gemm_split(_ptr(a), _ptr(b), _ptr(sa), int(sa.numel()), _ptr(sb),
                                      int(sb.numel()), _ptr(bias), _ptr(out), M, N, K, W, W,
                                      M * W, _stream(a.device))

@@ -33,6 +33,7 @@ from __future__ import annotations
 
 import torch
 
+from . import _lib
 from .kv_ring import KVRing
 from .model import rope_table
 
@@ -276,7 +277,7 @@ class StreamingRefiner:
                 fn(geom)  # plans, device tables, library handles: outside capture
                 torch.cuda.synchronize(self.device)
                 graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph):
+                with torch.cuda.graph(graph, stream=_lib.capture_stream(self.device)):
                     out = fn(geom)
                 entry = self._graphs[key] = (graph, out)
             entry[0].replay()

@@ -275,6 +275,31 @@ int srdit_fp8_gemm_ex(const void* a, const void* b, const float* sa, int64_t sa_
                       int64_t M, int64_t N, int64_t K, int64_t ldo, int epilogue,
                       uint32_t* amax_out, void* stream);
 
+/* Bytes of workspace with which srdit_fp8_gemm_ws may split any GEMM's last
+ * round of tiles (256 workgroups of fp32 partials and the counters). */
+#define SRDIT_GEMM_WS_BYTES ((int64_t)4096 + (int64_t)256 * 262144)
+
+/*
+ * srdit_fp8_gemm_ex with the output split of srdit_fp8_gemm_split (split_n 0:
+ * none) and a workspace (nullable) for a split-K tail: when the tiles of the
+ * output leave the last round of the persistent launch nearly empty and K is
+ * long (10800 x 3072 x 14336: 516 tiles, two rounds of 256 CUs and 4 tiles of
+ * 112 K stages), those tiles run in a second launch, each split along K over
+ * a few workgroups whose fp32 partials are summed in K order by the last of
+ * them to finish.  The results
+ * differ from the unsplit GEMM's only by the fp32 summation order.  The
+ * workspace (16-byte aligned, device) must hold zeros in its first 4096 bytes
+ * when first used (every call leaves them zero); up to workspace_bytes of it
+ * are used, SRDIT_GEMM_WS_BYTES allows every split.  Calls that share a
+ * workspace must be ordered (one stream).  Replaces what srdit_fp8_gemm_ex
+ * and srdit_fp8_gemm_split do (fp8_linear.py:282-297; models.py:1035-1062).
+ */
+int srdit_fp8_gemm_ws(const void* a, const void* b, const float* sa, int64_t sa_rows,
+                      const float* sb, int64_t sb_cols, const void* bias, void* out,
+                      int64_t M, int64_t N, int64_t K, int64_t ldo, int epilogue,
+                      uint32_t* amax_out, int64_t split_n, int64_t split_stride,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
 /*
  * The quantise pass of srdit_fp8_quant_tensor alone: amax_ws already holds the
  * bits of max |x| (written by a producer: srdit_ln_modulate or

@@ -120,3 +120,25 @@ def test_dense_linears_reject_bad_layouts_without_gpu():
     assert rc == 1 and "K=12" in _lib.last_error()
     rc = lib.srdit_gemv_f32(fake, 8, fake, 16, None, 0, fake, 2, 1, 4, 16, None)
     assert rc == 1 and "leading" in _lib.last_error()
+
+
+def test_gemm_with_workspace_rejects_bad_arguments_without_gpu():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(4096)
+    args = (fake, fake, fake, 1, fake, 1, None, fake, 1024, 3072, 3072, 3072, 0, None)
+    # the workspace of the split-K tail is read by 16-byte loads
+    rc = lib.srdit_fp8_gemm_ws(*args, 0, 0, ctypes.c_void_p(4104), _lib.GEMM_WS_BYTES, None)
+    assert rc == 1 and "workspace" in _lib.last_error()
+    rc = lib.srdit_fp8_gemm_ws(*args, -256, 0, fake, _lib.GEMM_WS_BYTES, None)
+    assert rc == 1 and "split_n" in _lib.last_error()
+    # the output-split rules of srdit_fp8_gemm_split hold here too
+    rc = lib.srdit_fp8_gemm_ws(*args, 1000, 1024 * 3072, fake, _lib.GEMM_WS_BYTES, None)
+    assert rc == 1 and "split_n" in _lib.last_error()
+
+
+def test_gemm_workspace_size_matches_the_header():
+    text = open(os.path.join(os.path.dirname(__file__), "..", "include", "srdit_hip.h")).read()
+    m = re.search(r"#define SRDIT_GEMM_WS_BYTES \(\(int64_t\)(\d+) \+ \(int64_t\)(\d+) \* (\d+)\)",
+                  text)
+    assert m, "SRDIT_GEMM_WS_BYTES not found"
+    assert int(m.group(1)) + int(m.group(2)) * int(m.group(3)) == _lib.GEMM_WS_BYTES

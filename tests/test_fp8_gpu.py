@@ -303,6 +303,127 @@ def test_gemm_split_output_equals_per_block_gemms(rs):
         assert torch.equal(out[j], ref), j
 
 
+def _tail_tiles(M, N, K):
+    """Output tiles (row, column) of the GEMM's split-K tail on this device: the
+    last (T mod G) tiles of the raster order (groups of 4 tile rows, column-major
+    inside a group), T = 256x256 tiles, G = the CUs rounded down to 8, when that
+    tail is at most G / 8 and a split along K saves a quarter of the round
+    (chosen as the library's planner does; None when nothing is split)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count // 8 * 8
+    tm, tn = -(-M // 256), -(-N // 256)
+    T = tm * tn
+    grid = min(cus, -(-T // 8) * 8)
+    tail, nks = T % grid, K // 128
+    if T < grid or tail == 0 or 8 * tail > grid:
+        return None
+    costs = [(-(-nks // S) + 5.0 + 4.0 * S, S) for S in range(2, nks + 1) if tail * S <= grid]
+    if not costs or min(costs)[0] >= 0.75 * nks:
+        return None
+    tiles = []
+    for task in range(T - tail, T):
+        group, r = divmod(task, 4 * tn)
+        gsize = min(tm - 4 * group, 4)
+        tiles.append((4 * group + r % gsize, r // gsize))
+    return tiles
+
+
+TAIL_CASES = [
+    # M, N, K, row-wise scales, GELU epilogue with the output amax: a streamed
+    # chunk's 10,800 rows leave the last round of tiles nearly empty (516 tiles,
+    # 4 in the last round); the split pays at long K
+    (10800, 3072, 14336, False, False),   # FFN down: 112 K stages per tile
+    (10800, 3072, 14336, True, True),     # row-wise scales, GELU + amax
+    (10800, 3072, 8192, False, False),    # 64 K stages
+]
+
+
+@pytest.mark.parametrize("M,N,K,rs,gelu", TAIL_CASES, ids=lambda v: str(v))
+def test_gemm_split_k_tail(M, N, K, rs, gelu):
+    """The split-K tail (srdit_fp8_gemm_ws): within the bound of the dequantised
+    product; every tile outside the tail bit for bit the unsplit GEMM's; the
+    tail's tiles within one bf16 rounding of it (fp8 products sum exactly in
+    fp32 for the most part, so they are mostly equal); the amax word exact; two
+    calls in a row (the arrival counters left at zero) bit for bit alike; two
+    launches with the split, one without."""
+    print(f"[case] gemm split-K tail M={M} N={N} K={K} rowwise={rs} gelu={gelu}", flush=True)
+    L = _lib()
+    g = torch.Generator("cpu").manual_seed(M + N + K)
+    a = (torch.randn(M, K, generator=g) * 0.6).to(F8).cuda()
+    b = (torch.randn(N, K, generator=g) * 0.6).to(F8).cuda()
+    if rs:
+        sa = (torch.rand(M, generator=g) + 0.5).cuda()
+        sb = (torch.rand(N, generator=g) / 64 + 1 / 128).cuda()
+    else:
+        sa, sb = torch.tensor([0.75]).cuda(), torch.tensor([1.25 / 64]).cuda()
+    bias = (torch.randn(N, generator=g) * 2).to(torch.bfloat16).cuda()
+    ep = 1 if gelu else 0
+    outs, amaxes = [], []
+    for split in (True, True, False):
+        out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        amax = torch.full((1,), 12345, dtype=torch.int32, device="cuda") if gelu else None
+        L.fp8_gemm_ex(a, b, sa, sb, bias, out, epilogue=ep, amax_out=amax, split_tail=split)
+        outs.append(out)
+        amaxes.append(amax)
+    torch.cuda.synchronize()
+    split1, split2, plain = outs
+    assert torch.equal(split1, split2)
+    if not gelu:
+        _dequant_check(split1, a, b, sa, sb, bias)
+    else:
+        assert amaxes[0].item() == split1.float().abs().max().view(torch.int32).item()
+        assert amaxes[2].item() == plain.float().abs().max().view(torch.int32).item()
+    tiles = _tail_tiles(M, N, K)
+    assert tiles, "this shape has a split tail on a 256-CU MI355X"
+    mask = torch.zeros(M, N, dtype=torch.bool, device="cuda")
+    for tr, tc in tiles:
+        mask[tr * 256:(tr + 1) * 256, tc * 256:(tc + 1) * 256] = True
+    assert torch.equal(split1[~mask], plain[~mask])
+    d = (split1[mask].float() - plain[mask].float()).abs()
+    assert (d <= 2.0 ** -7 * plain[mask].float().abs() + 1e-30).all(), d.max().item()
+    # the split ran: a second launch, the split instantiation of the kernel
+    from torch.profiler import ProfilerActivity, profile
+    for split, launches in ((True, 2), (False, 1)):
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            L.fp8_gemm_ex(a, b, sa, sb, bias, plain, epilogue=ep, amax_out=amaxes[2],
+                          split_tail=split)
+            torch.cuda.synchronize()
+        names = [ev.name for ev in prof.events()
+                 if ev.device_type == torch.autograd.DeviceType.CUDA and "fp8_gemm_kernel" in ev.name]
+        assert len(names) == launches, names
+
+
+def test_gemm_split_k_tail_split_output_and_graph():
+    """Three column blocks of one split-output GEMM with a split-K tail (1548
+    tiles, 12 in the last round, K = 8192), captured on the library's capture stream
+    and replayed on changing inputs with eager work between replays: every
+    replay bit for bit the eager call, each block within the bound of the
+    dequantised product."""
+    print("[case] gemm split-K tail, split output, graph", flush=True)
+    L = _lib()
+    M, K, W, G = 10800, 8192, 3072, 3
+    g = torch.Generator("cpu").manual_seed(23)
+    a = (torch.randn(M, K, generator=g) * 0.6).to(F8).cuda()
+    b = (torch.randn(G * W, K, generator=g) * 0.6).to(F8).cuda()
+    sa = torch.tensor([0.75]).cuda()
+    sb = torch.cat([torch.rand(1, generator=g).expand(W) for _ in range(G)]).contiguous().cuda()
+    bias = torch.randn(G * W, generator=g).to(torch.bfloat16).cuda()
+    assert _tail_tiles(M, G * W, K)
+    out = torch.empty((G, M, W), dtype=torch.bfloat16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=L.capture_stream("cuda")):
+        L.fp8_gemm_split(a, b, sa, sb, bias, out)
+    for it in range(3):
+        a.copy_((torch.randn(M, K, generator=g) * (0.3 + 0.3 * it)).to(F8).cuda())
+        graph.replay()
+        want = torch.empty_like(out)
+        L.fp8_gemm_split(a, b, sa, sb, bias, want)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), it
+    for j in range(G):
+        _dequant_check(out[j], a, b[j * W:(j + 1) * W], sa, sb[j * W:(j + 1) * W],
+                       bias[j * W:(j + 1) * W])
+
+
 def test_fp8_linear_rowwise_and_tensor():
     from sr_dit.fp8_linear import Fp8Linear
     torch.manual_seed(0)
