@@ -238,10 +238,10 @@ __device__ __forceinline__ i32x8_t read_frag(const uint8_t* lds, int off_lo, int
 // a function of the 16 bits of a bf16 x, so the per-tensor GELU quantiser looks
 // h up in a 65,536-entry table instead of evaluating tanhf per element (the
 // passes were bound by tanhf).  gelu_lut_build_kernel writes the table (one
-// entry per thread, the same gelu_tanh and bf16 rounding as the GEMM epilogue);
-// each workgroup of the two passes copies it into LDS (128 KB: one workgroup
-// per CU) and looks every element up there.  Pass 1 reduces max |h| (and stores
-// h when asked); pass 2 quantises h with the scale of that amax.
+// entry per thread, the same gelu_tanh and bf16 rounding as the GEMM epilogue).
+// Pass 1 copies it into LDS (128 KB: one workgroup per CU), looks every element
+// up there and reduces max |h| (and stores h when asked); pass 2 turns it into
+// a table of codes at the scale of that amax and looks the codes up.
 constexpr int LUT_N = 65536;
 constexpr int LUT_WAVES = 16;  // wavefronts per workgroup of the table passes
 
@@ -338,19 +338,21 @@ __global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_amax_kernel(
   }
 }
 
-// The quantise pass's walk for one wavefront.  It takes groups of 64 GQ
-// chunks, (row, base) with base a multiple of 64 GQ, row by row.  Two register
-// sets alternate, so the loads of the next group are in flight while the
-// current one is looked up, converted and stored, across row ends too.  A
-// clamped index re-reads a chunk of the row; it is not stored.  FAST: the
-// divisor's reciprocal is normal (tested once, not per element).
-constexpr int GQ = 8;  // chunks per lane per group: the table leaves one workgroup per CU
+// The quantise pass's walk for one wavefront takes groups of 64 GQ chunks,
+// (row, base) with base a multiple of 64 GQ, row by row.  Two register sets
+// alternate, so the loads of the next group are in flight while the current
+// one is looked up and stored, across row ends too.  A clamped index re-reads
+// a chunk of the row; it is not stored.
+constexpr int GQ = 8;  // chunks per lane per group
 
-template <bool FAST>
-__device__ __forceinline__ void gelu_quant_walk(const uint16_t* __restrict__ x, int64_t M,
-                                                int64_t K, int64_t ldx, const uint16_t* tab,
-                                                uint8_t* __restrict__ xq, const SharedDivisor& sd,
-                                                int64_t first_row, int64_t row_step, int lane) {
+// The quantise pass through a table of codes: every workgroup first writes the
+// e4m3 code of each of the 65,536 bf16 inputs at this call's scale into LDS
+// (64 KB, from the h table and the same conversion the per-element pass makes,
+// so the codes are the same), then each element of x is one byte lookup.
+__device__ __forceinline__ void code_walk(const uint16_t* __restrict__ x, int64_t M, int64_t K,
+                                          int64_t ldx, const uint8_t* codes,
+                                          uint8_t* __restrict__ xq, int64_t first_row,
+                                          int64_t row_step, int lane) {
   const int64_t nchunk = K >> 3;
   struct Pos {
     int64_t row, base;
@@ -368,20 +370,18 @@ __device__ __forceinline__ void gelu_quant_walk(const uint16_t* __restrict__ x, 
       v[u] = xr[c < nchunk ? c : nchunk - 1];
     }
   };
+  auto look = [&](uint32_t w) __attribute__((always_inline)) -> uint32_t {
+    return static_cast<uint32_t>(codes[w & 0xffffu]) |
+           (static_cast<uint32_t>(codes[w >> 16]) << 8);
+  };
   auto quant = [&](Pos p, const uint4 (&v)[GQ]) __attribute__((always_inline)) {
     uint2* qr = reinterpret_cast<uint2*>(xq + p.row * K);
 #pragma unroll
     for (int u = 0; u < GQ; ++u) {
-      const uint4 hv = lut8(tab, v[u]);
-      const uint32_t w[4] = {hv.x, hv.y, hv.z, hv.w};
-      float f[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f[2 * i] = __uint_as_float(w[i] << 16);
-        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-      }
+      const uint2 q = make_uint2(look(v[u].x) | (look(v[u].y) << 16),
+                                 look(v[u].z) | (look(v[u].w) << 16));
       const int64_t c = p.base + lane + 64 * u;
-      if (c < nchunk) qr[c] = to_e4m3x8<FAST>(f, sd);
+      if (c < nchunk) qr[c] = q;
     }
   };
   Pos pa{first_row, 0};
@@ -402,20 +402,32 @@ __device__ __forceinline__ void gelu_quant_walk(const uint16_t* __restrict__ x, 
   }
 }
 
-__global__ __launch_bounds__(64 * LUT_WAVES) void gelu_lut_quant_kernel(
+__global__ __launch_bounds__(64 * LUT_WAVES) void gelu_code_quant_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t ldx,
     const uint16_t* __restrict__ lut, uint8_t* __restrict__ xq, float* __restrict__ scale,
     const uint32_t* __restrict__ amax_ws) {
-  __shared__ __attribute__((aligned(16))) uint16_t tab[LUT_N];
-  load_lut_to_lds(tab, lut);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(16))) uint8_t codes[LUT_N];
   const float s = scale_from_amax_bits(*amax_ws);
   const SharedDivisor sd(s);
   if (blockIdx.x == 0 && threadIdx.x == 0) scale[0] = s;
+  // the code of input bits i: e4m3(h(i) / s), eight entries per 16-byte read of h
+  const uint4* src = reinterpret_cast<const uint4*>(lut);
+  for (int i = threadIdx.x; i < LUT_N / 8; i += blockDim.x) {
+    const uint4 hv = src[i];
+    const uint32_t w[4] = {hv.x, hv.y, hv.z, hv.w};
+    float f[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      f[2 * k] = __uint_as_float(w[k] << 16);
+      f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+    reinterpret_cast<uint2*>(codes)[i] = sd.fast ? to_e4m3x8<true>(f, sd) : to_e4m3x8<false>(f, sd);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t first = (int64_t)blockIdx.x * LUT_WAVES + wave;
   const int64_t step = (int64_t)gridDim.x * LUT_WAVES;
-  if (sd.fast) gelu_quant_walk<true>(x, M, K, ldx, tab, xq, sd, first, step, lane);
-  else gelu_quant_walk<false>(x, M, K, ldx, tab, xq, sd, first, step, lane);
+  code_walk(x, M, K, ldx, codes, xq, first, step, lane);
 }
 
 // ------------------------------------------------------------------ the GEMM
@@ -1184,10 +1196,10 @@ int quant_tensor_gelu(const void* x, int64_t M, int64_t K, int64_t ldx, void* h,
       static_cast<const uint16_t*>(x), M, K, ldx, static_cast<uint16_t*>(h), ldh,
       static_cast<const uint16_t*>(lut), amax_ws, h ? nullptr : xmax_pos);
   SRDIT_LAUNCH_CHECK("gelu_lut_amax_kernel");
-  gelu_lut_quant_kernel<<<blocks, 64 * LUT_WAVES, 0, s>>>(
+  gelu_code_quant_kernel<<<blocks, 64 * LUT_WAVES, 0, s>>>(
       static_cast<const uint16_t*>(x), M, K, ldx, static_cast<const uint16_t*>(lut),
       static_cast<uint8_t*>(xq), scale, amax_ws);
-  SRDIT_LAUNCH_CHECK("gelu_lut_quant_kernel");
+  SRDIT_LAUNCH_CHECK("gelu_code_quant_kernel");
   return SRDIT_OK;
 }
 }  // namespace

@@ -540,6 +540,32 @@ def test_gelu_table_covers_every_bf16_value():
     print(f"[metrics] gelu table: {int(ok.sum())} finite-or-inf outputs bit-exact, "
           f"{int(nan_w.sum())} NaN", flush=True)
 
+@pytest.mark.parametrize("bound", [0.5, 8.0, 300.0])
+def test_gelu_codes_for_every_bf16_input(bound):
+    """The quantise pass's codes (a table of the 65,536 inputs' codes at the
+    call's scale, looked up per element) against torch's GELU followed by the
+    plain per-tensor quantiser, bit for bit, for every finite bf16 x with
+    |x| <= bound (the bound sets the scale, so the codes span the e4m3 range)."""
+    from sr_dit import _lib
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    xs = bits[torch.isfinite(bits.float()) & (bits.float().abs() <= bound)]
+    n = xs.numel()
+    pad = (-n) % 512
+    x = torch.cat([xs, xs[:pad]]).reshape(-1, 512).to(DEV)
+    h = F.gelu(x.float(), approximate="tanh").to(torch.bfloat16)
+    want_q = torch.empty(x.shape, dtype=F8, device=DEV)
+    want_s = torch.empty(1, dtype=torch.float32, device=DEV)
+    _lib.fp8_quant_tensor(h, want_q, want_s, torch.zeros(1, dtype=torch.int32, device=DEV))
+    got_q = torch.empty_like(want_q)
+    got_s = torch.empty_like(want_s)
+    _lib.fp8_quant_tensor_gelu(x, got_q, got_s, torch.zeros(1, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    print(f"[metrics] {n} inputs, scale {got_s.item():.4e}, "
+          f"{int(torch.unique(got_q.view(torch.uint8)).numel())} distinct codes", flush=True)
+    assert torch.equal(got_s, want_s)
+    assert torch.equal(got_q.view(torch.uint8), want_q.view(torch.uint8))
+
+
 def test_gelu_amax_shortcut_holds_over_every_bf16_value():
     """The facts the amax shortcut rests on, over all 65,536 bf16 inputs of the
     table: h = bf16(gelu(x)) is non-decreasing over x >= 0, and |h| below 0 stays
