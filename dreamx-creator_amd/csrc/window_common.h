@@ -99,6 +99,19 @@ __device__ __forceinline__ void buffer_load_lds_x4(__amdgpu_buffer_rsrc_t rsrc, 
       rsrc, (__attribute__((address_space(3))) void*)lds, 16, index, offset, 0, 0, 0);
 }
 
+// 16 bytes per lane from record `index`, byte `offset` of the structured
+// buffer `rsrc` straight into LDS at byte address lds + 16 * lane
+// (buffer_load_dwordx4 ... idxen offen lds).  Written as inline asm so the
+// compiler does not treat it as an LDS store: it would otherwise wait for
+// every outstanding fill before any later LDS read.  Callers fill only LDS
+// that no wavefront is reading, and order the fills before the reads of the
+// data with explicit waits and a barrier.
+__device__ __forceinline__ void dma_x4(i32x4_t rsrc, uint32_t lds, int index, int offset) {
+  const i32x2_t va = {index, offset};
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 idxen offen lds" ::"v"(va), "s"(rsrc), "{m0}"(lds)
+               : "memory");
+}
+
 // Compiler-only fence: keeps LDS/DMA accesses on their side of a wait or a
 // barrier without emitting any wait of its own.
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }

@@ -54,19 +54,6 @@ struct GroupArgs {
 
 constexpr int GKN = 32;  // keys per block
 
-// 16 bytes per lane from record `index`, byte `offset` of the structured
-// buffer `rsrc` straight into LDS at byte address lds + 16 * lane
-// (buffer_load_dwordx4 ... idxen offen lds).  Written as inline asm so the
-// compiler does not treat it as an LDS store: it would otherwise wait for
-// every outstanding fill before any later LDS read.  The fills only ever
-// target the ring stage no wavefront is reading, and fill_barrier's explicit
-// full wait orders them before the reads of the next step.
-__device__ __forceinline__ void dma_x4(i32x4_t rsrc, uint32_t lds, int index, int offset) {
-  const i32x2_t va = {index, offset};
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 idxen offen lds" ::"v"(va), "s"(rsrc), "{m0}"(lds)
-               : "memory");
-}
-
 // The frames a member consumes in private slots: [lo1, lo1+len1) then
 // [lo2, lo2+len2) -- its frame range minus the frames shared with the partner.
 struct PrivFrames {

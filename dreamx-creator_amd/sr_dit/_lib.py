@@ -40,6 +40,8 @@ SIGNATURES = {
                                               _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64,
                                               _c_int, _c_int, _c_f, _c_int, _c_int, _c_p,
                                               _c_p, _c_int, _c_p]),
+    "srdit_dense_attn_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_int, _c_int,
+                                      _c_f, _c_p, _c_int, _c_p]),
     "srdit_fp8_quant_rowwise": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p]),
     "srdit_fp8_quant_tensor": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p,
                                         _c_p]),
@@ -184,6 +186,26 @@ def window_attn_packed_fwd(q, k, v, o, params, tiles, *, n_w, hr_base, H, W, n_h
     _check(load().srdit_window_attn_packed_fwd(*args, *_ex_args(ring, amax_out),
                                                DTYPE_CODES[q.dtype], _stream(q.device)),
            "srdit_window_attn_packed_fwd")
+
+
+def dense_attn_fwd(q, k, v, o, scale, amax_out=None):
+    """Every query of ``q`` [Lq, H, D] attends every key of ``k``/``v`` [Lkv, H, D]
+    of its head into ``o`` [Lq, H, D] (srdit_dense_attn_fwd); ``amax_out``
+    (int32 [1], nullable) receives the bits of max |o|."""
+    if q.dtype not in DTYPE_CODES:
+        raise ValueError(f"dense attention needs bf16 or fp16, got {q.dtype}")
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+        if t.dim() != 3 or not t.is_contiguous() or t.dtype != q.dtype or t.device != q.device:
+            raise ValueError(f"dense_attn_fwd: {name} must be a contiguous 3-D {q.dtype} tensor "
+                             f"on {q.device}")
+    if k.shape != v.shape or k.shape[1:] != q.shape[1:] or o.shape != q.shape:
+        raise ValueError(f"dense_attn_fwd: shapes q {tuple(q.shape)}, k {tuple(k.shape)}, "
+                         f"v {tuple(v.shape)}, o {tuple(o.shape)} do not match")
+    _check(load().srdit_dense_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), int(q.shape[0]),
+                                       int(k.shape[0]), int(q.shape[1]), int(q.shape[2]),
+                                       float(scale), _ptr(amax_out), DTYPE_CODES[q.dtype],
+                                       _stream(q.device)),
+           "srdit_dense_attn_fwd")
 
 
 QUANT_DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

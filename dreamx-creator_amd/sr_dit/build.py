@@ -29,6 +29,7 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
 # mirrored between AGPRs and VGPRs every step.  The GEMM keeps the default.
 FILE_FLAGS = {"window_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
               "window_group.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+              "dense_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
               # the fused elementwise kernels round after every operation, as
               # torch's separate kernels do: no multiply-add contraction
               "fused.hip": ["-ffp-contract=off"]}

@@ -152,6 +152,11 @@ def sinusoidal_embedding_1d(dim, position):
     return torch.cat([ang.cos(), ang.sin()], dim=1)
 
 
+#: Cross-attention on the persistent dense kernel (srdit_dense_attn_fwd);
+#: False runs it on the window kernel as a 1 x Lq grid of 64-query windows.
+DENSE_CROSS = True
+
+
 class CrossAttentionPlan:
     """Dense attention of Lq video tokens over Lc context tokens on the window kernel.
 
@@ -172,8 +177,16 @@ class CrossAttentionPlan:
                      "p_stride": bgh.P_PLAIN}
 
     def run(self, q, k, v, out, amax_out=None):
+        """out = softmax(q k^T d^-1/2) v per head.  On the dense kernel
+        (srdit_dense_attn_fwd) when ``DENSE_CROSS`` is set and the shapes fit it,
+        else on the window kernel with this plan."""
+        d = q.shape[2]
+        if DENSE_CROSS and d in (64, 128) and q.dtype in (torch.bfloat16, torch.float16) \
+                and all(t.is_contiguous() for t in (q, k, v, out)) and k.shape[0] == self.lc:
+            _lib.dense_attn_fwd(q, k, v, out, d ** -0.5, amax_out)
+            return out
         bgh.run_blockgrid_hip(q, k, v, out, plan=self.plan, f_cur=1, h=1, w=self.lq,
-                              n=q.shape[1], d=q.shape[2], amax_out=amax_out)
+                              n=q.shape[1], d=d, amax_out=amax_out)
         return out
 
 

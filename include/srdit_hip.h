@@ -158,6 +158,23 @@ int srdit_window_attn_packed_fwd(const void* q, const void* k, const void* v, vo
                                  void* stream);
 
 /*
+ * Dense attention: o[i, h] = softmax(q[i, h] . k[:, h]^T * scale) v[:, h] for
+ * every query token i and head h, over all kv_tokens keys.  q and o are
+ * [q_tokens, n_heads, head_dim], k and v [kv_tokens, n_heads, head_dim], all
+ * contiguous.  Replaces the attention of WanT2VCrossAttention.forward
+ * (models.py:1042-1062): the video tokens' queries over the text context's
+ * keys and values.  Persistent workgroups that prefetch the next 128 queries
+ * while the current ones run; the numerics of the window kernels (q scaled by
+ * scale*log2(e) and rounded once, base-2 softmax, P rounded to the input type,
+ * fp32 accumulation).  amax_out (nullable): cleared, then max |o| (fp32 bits).
+ * head_dim 64 or 128, bf16 or fp16, token strides below 16384 bytes, Q/O and
+ * K/V below 2^31 bytes each.
+ */
+int srdit_dense_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                         int64_t q_tokens, int64_t kv_tokens, int n_heads, int head_dim,
+                         float scale, uint32_t* amax_out, int dtype, void* stream);
+
+/*
  * Row-wise fp8 e4m3 quantiser: for each row of x [M, K] (row stride ldx),
  *   scale[m] = max(amax(|x[m,:]|) * fl32(1/448), 1e-12)   (fp32; what torch computes
  *              for amax / 448.0 on a GPU tensor)

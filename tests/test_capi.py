@@ -142,3 +142,18 @@ def test_gemm_workspace_size_matches_the_header():
                   text)
     assert m, "SRDIT_GEMM_WS_BYTES not found"
     assert int(m.group(1)) + int(m.group(2)) * int(m.group(3)) == _lib.GEMM_WS_BYTES
+
+
+def test_dense_attention_rejects_bad_arguments_without_gpu():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(4096)
+    rc = lib.srdit_dense_attn_fwd(fake, fake, fake, ctypes.c_void_p(4100), 100, 512, 24, 128,
+                                  0.088, None, 0, None)
+    assert rc == 1 and "aligned" in _lib.last_error()
+    rc = lib.srdit_dense_attn_fwd(fake, fake, fake, fake, 100, 0, 24, 128, 0.088, None, 0, None)
+    assert rc == 1 and "kv_tokens" in _lib.last_error()
+    rc = lib.srdit_dense_attn_fwd(fake, fake, fake, fake, 100, 512, 24, 96, 0.088, None, 0, None)
+    assert rc == 3 and "head_dim" in _lib.last_error()
+    rc = lib.srdit_dense_attn_fwd(fake, fake, fake, fake, 1 << 20, 512, 24, 128, 0.088, None, 0,
+                                  None)
+    assert rc == 1 and "2^31" in _lib.last_error()
