@@ -119,7 +119,7 @@ def profile_traffic(config):
         return None, f"{rel} holds no traffic figure"
     if not hm or hm.group(1) != cur:
         return None, (f"stale: {rel} measured sources {hm.group(1) if hm else '(unstamped)'}, "
-                      f"this build's are {cur}")
+                      f"the current sources are {cur}")
     return float(m.group(1)), f"{rel} (FETCH_SIZE + WRITE_SIZE, sources {cur})"
 
 

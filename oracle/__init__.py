@@ -2,8 +2,9 @@
 fp8-linear path.  TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker (or the timed CPU
-baseline) -- never as the thing measured or shipped.  The product path in
+``bench.py`` may import this package, and only as the reference that outputs are
+compared against (or the timed CPU baseline) -- never as the thing measured or
+shipped.  The product path in
 ``dreamx-creator_amd/sr_dit`` must not import it and has no CPU fallback.
 
 Modules

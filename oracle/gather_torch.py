@@ -11,8 +11,8 @@ the GPU, as the reference for full-size parity tests.  There the tests pass
 softmax(q k^T * scale) v in the input dtype), so no fused or memory-efficient
 kernel of the library stands between the reference and the formula; a GPU test
 checks sampled windows of that reference against the float64 oracle
-(oracle/blockgrid.py).  It is the checker, not the product: nothing under
-dreamx-creator_amd/ imports it.
+(oracle/blockgrid.py).  It is test infrastructure, not the product: nothing
+under dreamx-creator_amd/ imports it.
 """
 from __future__ import annotations
 
