@@ -557,21 +557,24 @@ void fp8_gemm_kernel(const GemmArgs g) {
                  : "memory");
   };
   int f_t = 0, f_kt = 0, f_slot = 0;  // fill cursor: tile, stage in tile, slot
+  int f_m0 = 0, f_n0 = 0;             // the cursor tile's first row and column
   i32x4_t f_ra = {}, f_rb = {};
   auto fill_next = [&]() __attribute__((always_inline)) {
-    int m0, n0;
-    coords(f_t, m0, n0);
+    // The tile's coordinates, once per tile (its integer divisions would
+    // otherwise run after every stage's barrier).
+    if (f_kt == 0) {
+      coords(f_t, f_m0, f_n0);
+      f_ra = rsrc_of(g.a + (int64_t)f_m0 * g.K, (int64_t)(g.M - f_m0) * g.K);
+      f_rb = rsrc_of(g.b + (int64_t)f_n0 * g.K, (int64_t)(g.N - f_n0) * g.K);
+    }
     if (f_kt == nks - 1 && wave < 3) {  // the tile's epilogue data, ahead of its last stage
+      const int m0 = f_m0, n0 = f_n0;
       i32x4_t r;
       if (wave == 0) r = rsrc_of(g.sa + m0, g.sa_per_row ? (int64_t)(g.M - m0) * 4 : 0);
       else if (wave == 1) r = rsrc_of(g.sb + n0, g.sb_per_col ? (int64_t)(g.N - n0) * 4 : 0);
       else r = rsrc_of(g.bias ? (const void*)(g.bias + n0) : (const void*)g.b,
                        g.bias ? (int64_t)(g.N - n0) * 2 : 0);
       dma(r, 16 * lane, 0, lds_base + G_EPI_OFF + (f_t % 3) * G_EPI_REG + wave * 1024);
-    }
-    if (f_kt == 0) {
-      f_ra = rsrc_of(g.a + (int64_t)m0 * g.K, (int64_t)(g.M - m0) * g.K);
-      f_rb = rsrc_of(g.b + (int64_t)n0 * g.K, (int64_t)(g.N - n0) * g.K);
     }
     const uint32_t base = lds_w + f_slot * G_SLOT;
     const int koff = (k_first + f_kt) * G_FK;
