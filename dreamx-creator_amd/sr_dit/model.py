@@ -104,6 +104,41 @@ def rope_params(max_seq_len, dim, theta=10000.0):
     return torch.polar(torch.ones_like(ang), ang)
 
 
+def rope_positions(cfg: SRDiTConfig, f, h, w, t_offset=0, hw_stride=(1, 1)) -> int:
+    """Positions the per-axis tables of a (f, h, w) grid need: they reach
+    t_offset + f - 1 and (h - 1) * s_h, (w - 1) * s_w, and grow in whole
+    multiples of rope_max_seq_len, as _ensure_rope_freqs (models.py:1789-1809)
+    extends the reference's cache."""
+    s_h, s_w = (int(hw_stride[0]), int(hw_stride[1]))
+    need = max(int(t_offset) + f, s_h * h, s_w * w, 1)
+    base = int(cfg.rope_max_seq_len)
+    return base * -(-need // base)
+
+
+def rope_axis_tables(cfg: SRDiTConfig, n_pos, device="cpu"):
+    """The (t, h, w) frequency tables of rope_apply (models.py:176-178), each
+    complex64 [n_pos, pairs]: c = head_dim/2 complex pairs split
+    [c - 2(c//3), c//3, c//3], computed in float64 and rounded once."""
+    dt, dh, dw = rope_axis_dims(cfg.head_dim)
+    return tuple(rope_params(n_pos, dx, cfg.rope_theta).to(torch.complex64).to(device)
+                 for dx in (dt, dh, dw))
+
+
+def rope_table_from_axes(axes, f, h, w, t_offset=0, hw_stride=(1, 1)):
+    """Per-token rotation [f*h*w, 1, head_dim/2] gathered from per-axis tables
+    (rope_axis_tables) on their device: frame t_offset + i, row i*s_h, column
+    j*s_w.  Only copies, so the result is the same on any device."""
+    ft, fh, fw = axes
+    s_h, s_w = (int(hw_stride[0]), int(hw_stride[1]))
+    c = ft.shape[1] + fh.shape[1] + fw.shape[1]
+    if t_offset + f > ft.shape[0] or s_h * (h - 1) >= fh.shape[0] or s_w * (w - 1) >= fw.shape[0]:
+        raise ValueError("rope_table_from_axes: the axis tables are too short for this grid")
+    return torch.cat([
+        ft[t_offset:t_offset + f].view(f, 1, 1, -1).expand(f, h, w, -1),
+        fh[0:s_h * h:s_h].view(1, h, 1, -1).expand(f, h, w, -1),
+        fw[0:s_w * w:s_w].view(1, 1, w, -1).expand(f, h, w, -1)], dim=-1).reshape(f * h * w, 1, c)
+
+
 def rope_table(cfg: SRDiTConfig, f, h, w, t_offset=0, device="cuda", hw_stride=(1, 1)):
     """Per-token complex64 rotation [f*h*w, 1, head_dim/2] for a (f, h, w) grid.
 
@@ -115,24 +150,8 @@ def rope_table(cfg: SRDiTConfig, f, h, w, t_offset=0, device="cuda", hw_stride=(
     s_h, s_w = (int(hw_stride[0]), int(hw_stride[1]))
     if s_h < 1 or s_w < 1:
         raise ValueError(f"rope_table: hw_stride must be >= 1, got {hw_stride!r}")
-    d = cfg.head_dim
-    dt, dh, dw = rope_axis_dims(d)
-    c = d // 2
-    # positions reach t_offset + f - 1 and (h - 1) * s_h, (w - 1) * s_w: the table
-    # grows in whole multiples of rope_max_seq_len, as _ensure_rope_freqs
-    # (models.py:1789-1809) extends the reference's cache
-    need = max(int(t_offset) + f, s_h * h, s_w * w, 1)
-    base = int(cfg.rope_max_seq_len)
-    n_pos = base * -(-need // base)
-    ft = rope_params(n_pos, dt, cfg.rope_theta)
-    fh = rope_params(n_pos, dh, cfg.rope_theta)
-    fw = rope_params(n_pos, dw, cfg.rope_theta)
-    assert ft.shape[1] + fh.shape[1] + fw.shape[1] == c
-    tab = torch.cat([
-        ft[t_offset:t_offset + f].view(f, 1, 1, -1).expand(f, h, w, -1),
-        fh[0:s_h * h:s_h].view(1, h, 1, -1).expand(f, h, w, -1),
-        fw[0:s_w * w:s_w].view(1, 1, w, -1).expand(f, h, w, -1)], dim=-1).reshape(f * h * w, 1, c)
-    return tab.to(torch.complex64).to(device)
+    axes = rope_axis_tables(cfg, rope_positions(cfg, f, h, w, t_offset, hw_stride))
+    return rope_table_from_axes(axes, f, h, w, t_offset, hw_stride).to(device)
 
 
 def rope_apply(x, table):

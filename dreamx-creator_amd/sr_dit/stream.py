@@ -35,7 +35,7 @@ import torch
 
 from . import _lib
 from .kv_ring import KVRing
-from .model import rope_table
+from .model import rope_axis_tables, rope_positions, rope_table_from_axes
 
 
 class FlowMatchSchedule:
@@ -162,6 +162,11 @@ class StreamingRefiner:
                                        2 * self.anchor_hw[1], dtype=torch.float32, device=self.device)
         self._e = torch.zeros(1, cfg.dim, dtype=torch.float32, device=self.device)
         self._e0 = torch.zeros(1, 6, cfg.dim, dtype=torch.float32, device=self.device)
+        # A forward's timestep and RoPE table reach the device by device-side
+        # writes: a blocking host-to-device copy would wait for the forwards
+        # already queued and leave the GPU idle while the host prepares the next.
+        self._t_dev = torch.zeros(1, dtype=torch.float32, device=self.device)
+        self._rope_axes = None  # per-axis RoPE tables on the device (rope_axis_tables)
         self._geoms = {}
         self._graphs = {}
         self.forwards = 0
@@ -204,12 +209,22 @@ class StreamingRefiner:
             g["ring_cat"] = self.ring_cat
         elif g["t_offset"] != t_offset:
             f, gh, gw = g["grid"]
-            rope = rope_table(self.model.cfg, f, gh, gw, t_offset, self.device,
-                              hw_stride=g["hw_stride"])
+            rope = self._rope_on_device(f, gh, gw, t_offset, g["hw_stride"])
             g["rope"].copy_(rope)
             g["rope_cs"].copy_(torch.view_as_real(rope).reshape(g["rope_cs"].shape))
             g["t_offset"] = t_offset
         return g
+
+    def _rope_on_device(self, f, h, w, t_offset, hw_stride):
+        """The RoPE table of a (f, h, w) grid at frame offset ``t_offset``,
+        gathered on the device from per-axis tables kept there (the same values
+        as model.rope_table); the tables are rebuilt only when a position runs
+        past them."""
+        cfg = self.model.cfg
+        n_pos = rope_positions(cfg, f, h, w, t_offset, hw_stride)
+        if self._rope_axes is None or self._rope_axes[0].shape[0] < n_pos:
+            self._rope_axes = rope_axis_tables(cfg, n_pos, self.device)
+        return rope_table_from_axes(self._rope_axes, f, h, w, t_offset, hw_stride)
 
     def _run(self, geom):
         return self.model.forward_embedded(self._lat, self._e, self._e0, self.ctx, geom,
@@ -264,7 +279,8 @@ class StreamingRefiner:
 
     def _launch(self, key, t, latent, t_offset, fn):
         with torch.no_grad():
-            e, e0 = self.model.time_embed(torch.tensor([float(t)], device=self.device))
+            self._t_dev.fill_(float(t))
+            e, e0 = self.model.time_embed(self._t_dev)
             self._e.copy_(e)
             self._e0.copy_(e0)
             (self._lat_lq if key[0] == "harvest" else self._lat).copy_(latent)

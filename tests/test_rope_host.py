@@ -71,3 +71,21 @@ def test_rope_apply_rotates_pairs():
         z = complex(a, b) * complex(tab[tok, 0, c])
         assert abs(float(y[tok, head, 2 * c]) - z.real) <= 1e-5
         assert abs(float(y[tok, head, 2 * c + 1]) - z.imag) <= 1e-5
+
+
+@pytest.mark.parametrize("t_offset,stride", [(0, (1, 1)), (27, (1, 1)), (1100, (1, 1)), (9, (2, 3))])
+def test_rope_table_from_longer_axis_tables(t_offset, stride):
+    """The streaming loop gathers a new offset's table on the device from axis
+    tables kept there, which may hold more positions than the grid needs: the
+    gather equals rope_table bit for bit, and refuses tables that are too short."""
+    cfg = mdl.SRDiTConfig()
+    f, h, w = 3, 9, 16
+    want = mdl.rope_table(cfg, f, h, w, t_offset, "cpu", hw_stride=stride)
+    n_pos = mdl.rope_positions(cfg, f, h, w, t_offset, stride)
+    for extra in (0, int(cfg.rope_max_seq_len)):
+        axes = mdl.rope_axis_tables(cfg, n_pos + extra)
+        got = mdl.rope_table_from_axes(axes, f, h, w, t_offset, stride)
+        assert torch.equal(torch.view_as_real(got), torch.view_as_real(want))
+    short = mdl.rope_axis_tables(cfg, t_offset + f - 1)
+    with pytest.raises(ValueError):
+        mdl.rope_table_from_axes(short, f, h, w, t_offset, stride)
